@@ -1,0 +1,101 @@
+"""ctypes binding of librq.so (include/rq.h).
+
+torch is imported before the library is opened: torch ships its own HIP
+runtime, and librq's libamdhip64.so.7 dependency must resolve to that same
+runtime (matching soname) so both share one HIP/HSA instance and device
+pointers. The library is required: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import torch  # noqa: F401  (loads the process's HIP runtime first)
+
+from .errors import BackendError, RllmError, ShapeError, UnsupportedError
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "librq.so")
+HEADER = os.path.join(os.path.dirname(PKG), "include", "rq.h")
+
+RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID = 0, 1, 2, 3, 4
+MATVEC_MAX_COLS = 8
+
+
+class Q8_1Struct(ctypes.Structure):
+    _fields_ = [
+        ("qs", ctypes.c_void_p),
+        ("d", ctypes.c_void_p),
+        ("s", ctypes.c_void_p),
+        ("len", ctypes.c_int64),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+_SIGNATURES = {
+    "rq_last_error": (ctypes.c_char_p, []),
+    "rq_open": (_int, [_int, ctypes.POINTER(_vp)]),
+    "rq_close": (_int, [_vp]),
+    "rq_set_stream": (_int, [_vp, _vp]),
+    "rq_device_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.c_char_p, ctypes.c_size_t]),
+    "rq_row_bytes": (_i64, [_int, _i64]),
+    "rq_upload": (_int, [_vp, _int, _i64, _i64, _vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "rq_weight_free": (_int, [_vp]),
+    "rq_weight_shape": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                               ctypes.POINTER(ctypes.c_size_t)]),
+    "rq_weight_to_gguf": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "rq_quantize_q8_1": (_int, [_vp, _vp, _i64, _i64, _i64, ctypes.POINTER(Q8_1Struct)]),
+    "rq_matvec": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
+    "rq_matvec_many": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                              ctypes.POINTER(_i64), _int]),
+    "rq_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _i64]),
+    "rq_matmul_many": (_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                              ctypes.POINTER(_i64), _int]),
+    "rq_reserve": (_int, [_vp, _i64]),
+    "rq_block_dots": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def declared_symbols(header: str = HEADER) -> list[str]:
+    """Function names declared in include/rq.h."""
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(rq_\w+)\s*\(", text, flags=re.M)))
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RllmError(f"{LIB_PATH} is not built; run `python -m rllm_amd.build` (no fallback path exists)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().rq_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int) -> None:
+    """Raise the rllm_core::Error kind matching a non-zero rq_status."""
+    if status == RQ_OK:
+        return
+    msg = last_error()
+    if status == RQ_ERR_SHAPE:
+        raise ShapeError(msg)
+    if status == RQ_ERR_UNSUPPORTED:
+        raise UnsupportedError(msg)
+    if status == RQ_ERR_BACKEND:
+        raise BackendError(msg)
+    raise RllmError(f"invalid argument: {msg}")

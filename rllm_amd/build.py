@@ -1,0 +1,82 @@
+"""Ahead-of-time build of librq.so for gfx950.
+
+1. hipcc --genco compiles csrc/rq_kernels.hip into one gfx950 code object.
+2. An assembler stub (.incbin) embeds that code object in the library.
+3. g++ compiles the host side (csrc/rq_host.cpp) against the HIP runtime.
+
+The result, rllm_amd/lib/librq.so, is self-contained: rq_open() loads the
+embedded code object with hipModuleLoadData; nothing is compiled at run time.
+
+Usage: python -m rllm_amd.build   (or rllm_amd.build.build()).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+LIBDIR = os.path.join(PKG, "lib")
+LIB = os.path.join(LIBDIR, "librq.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+# Device code: IEEE-correct f32 division (the Q8_1 scale and codes must match
+# the CPU bit for bit) and no packed-f32 instructions (they have given wrong
+# results on these machines).
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile everything; returns the library path."""
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIBDIR, exist_ok=True)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    hsaco = os.path.join(BUILD, "rq_kernels.hsaco")
+    _run([hipcc, "--genco", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_kernels.hip"), "-o", hsaco])
+    blob = os.path.join(BUILD, "rq_blob.S")
+    with open(blob, "w") as f:
+        f.write(
+            "    .section .rodata\n"
+            "    .balign 4096\n"
+            "    .globl rq_kernels_blob\n"
+            "    .type rq_kernels_blob, @object\n"
+            "rq_kernels_blob:\n"
+            f'    .incbin "{hsaco}"\n'
+            "    .byte 0\n"
+            "    .size rq_kernels_blob, . - rq_kernels_blob\n"
+            '    .section .note.GNU-stack,"",@progbits\n'
+        )
+    tmp = LIB + ".tmp"
+    _run([
+        "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",
+        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{CSRC}",
+        os.path.join(CSRC, "rq_host.cpp"), blob,
+        f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+        "-o", tmp,
+    ])
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)
