@@ -111,13 +111,25 @@ struct XUnit {
     int sb;     // sum of codes 16..31
 };
 
-template <int FMT>
-__device__ __forceinline__ void load_x(const int8_t* __restrict__ xq, const u16* __restrict__ xd, int u, XUnit& x) {
+// Raw loads of one activation unit (codes and f16 scale) ...
+__device__ __forceinline__ void load_x_raw(const int8_t* __restrict__ xq, const u16* __restrict__ xd, int u, XUnit& x) {
     const int4* p = (const int4*)(xq + (int64_t)u * 32);
     const int4 a = p[0], b = p[1];
     x.q[0] = a.x; x.q[1] = a.y; x.q[2] = a.z; x.q[3] = a.w;
     x.q[4] = b.x; x.q[5] = b.y; x.q[6] = b.z; x.q[7] = b.w;
-    x.dx = h2f(xd[u]);
+    x.sa = xd[u];  // f16 bits until prepare_x
+}
+
+// ... then the derived values: f32 scale and the code sums the offset and
+// min terms need. valid == false zeroes the unit, so it contributes nothing.
+template <int FMT>
+__device__ __forceinline__ void prepare_x(XUnit& x, bool valid = true) {
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) x.q[i] = 0;
+        x.sa = 0;
+    }
+    x.dx = h2f((u32)x.sa);
     x.sa = 0;
     x.sb = 0;
     x.dxs = 0.f;
@@ -132,6 +144,12 @@ __device__ __forceinline__ void load_x(const int8_t* __restrict__ xq, const u16*
         x.sb = sb;
         if (FMT == RQ_FMT_Q4_K) x.dxs = x.dx * (float)(sa + sb);
     }
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_x(const int8_t* __restrict__ xq, const u16* __restrict__ xd, int u, XUnit& x) {
+    load_x_raw(xq, xd, u, x);
+    prepare_x<FMT>(x);
 }
 
 // ---------------------------------------------------------------------------
@@ -252,7 +270,9 @@ __device__ __forceinline__ void mv_body(const RqMvParams& P) {
     constexpr int RPW = MvShape<NC>::RPW;
     constexpr int TC = MvShape<NC>::TC;
     const int lane = threadIdx.x & 63;
-    const int gwave = blockIdx.x * RQ_MV_WAVES + (threadIdx.x >> 6);
+    // Wave-uniform by construction; readfirstlane lets the compiler keep the
+    // target selection and row base in scalar registers (s_load from kernarg).
+    const int gwave = blockIdx.x * RQ_MV_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int ti = 0;
     if (P.count > 1 && gwave >= P.t[1].wave_start) ti = 1;
     if (P.count > 2 && gwave >= P.t[2].wave_start) ti = 2;
@@ -260,7 +280,7 @@ __device__ __forceinline__ void mv_body(const RqMvParams& P) {
     const int n = T.n;
     const int r0 = (gwave - T.wave_start) * RPW;
     if (r0 >= n) return;  // wave-uniform
-    const int k = P.k, U = k >> 5, m = P.m;
+    const int k = P.k, U = k >> 5;
     const int j_sb = lane & 7;  // unit index within its super-block (u = 64*i + lane)
 
     float acc[RPW][NC];
@@ -269,39 +289,52 @@ __device__ __forceinline__ void mv_body(const RqMvParams& P) {
 #pragma unroll
         for (int c = 0; c < NC; c++) acc[rr][c] = 0.f;
 
+    // Rows past the end are clamped to the last row (loaded, never stored);
+    // units past the end are clamped and their activation zeroed, so every
+    // load is unconditional and the whole chunk is in flight at once.
+    int rows[RPW];
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++) rows[rr] = min(r0 + rr, n - 1);
+
     for (int ub = 0; ub < U; ub += 64 * TC) {
-        XUnit xu[TC][NC];
+        int uc[TC];
+        bool valid[TC];
 #pragma unroll
         for (int t = 0; t < TC; t++) {
             const int u = ub + 64 * t + lane;
-#pragma unroll
-            for (int c = 0; c < NC; c++)
-                if (u < U && c < m) load_x<FMT>(P.xq + (int64_t)c * k, P.xd + (int64_t)c * U, u, xu[t][c]);
+            valid[t] = u < U;
+            uc[t] = valid[t] ? u : U - 1;
         }
+        // Weights first (the HBM stream), then the activation units (L2
+        // hits after the first wave): all loads of the chunk are issued
+        // before any arithmetic, so they share one memory round trip.
         WUnit wu[RPW][TC];
 #pragma unroll
         for (int rr = 0; rr < RPW; rr++)
 #pragma unroll
-            for (int t = 0; t < TC; t++) {
-                const int u = ub + 64 * t + lane;
-                if (r0 + rr < n && u < U) load_w<FMT>(T.w, r0 + rr, u, U, wu[rr][t]);
-            }
+            for (int t = 0; t < TC; t++) load_w<FMT>(T.w, rows[rr], uc[t], U, wu[rr][t]);
+        XUnit xu[TC][NC];
+#pragma unroll
+        for (int t = 0; t < TC; t++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) load_x_raw(P.xq + (int64_t)c * k, P.xd + (int64_t)c * U, uc[t], xu[t][c]);
+        // The scheduler would otherwise interleave loads with waits and
+        // serialize the round trips.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < TC; t++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) prepare_x<FMT>(xu[t][c], valid[t]);
 #pragma unroll
         for (int rr = 0; rr < RPW; rr++)
 #pragma unroll
-            for (int t = 0; t < TC; t++) {
-                const int u = ub + 64 * t + lane;
-                if (r0 + rr < n && u < U) {
+            for (int t = 0; t < TC; t++)
 #pragma unroll
-                    for (int c = 0; c < NC; c++) {
-                        if (c < m) {
-                            int s0, s1;
-                            unit_dots<FMT>(wu[rr][t], xu[t][c], s0, s1);
-                            acc[rr][c] += unit_value<FMT>(wu[rr][t], xu[t][c], j_sb, s0, s1);
-                        }
-                    }
+                for (int c = 0; c < NC; c++) {
+                    int s0, s1;
+                    unit_dots<FMT>(wu[rr][t], xu[t][c], s0, s1);
+                    acc[rr][c] += unit_value<FMT>(wu[rr][t], xu[t][c], j_sb, s0, s1);
                 }
-            }
     }
 
 #pragma unroll
@@ -309,7 +342,7 @@ __device__ __forceinline__ void mv_body(const RqMvParams& P) {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const float v = wave_sum(acc[rr][c]);
-            if (lane == 0 && r0 + rr < n && c < m) T.out[(int64_t)c * n + r0 + rr] = v;
+            if (lane == 0 && r0 + rr < n) T.out[(int64_t)c * n + r0 + rr] = v;
         }
 }
 
