@@ -2,28 +2,33 @@
 // the gfx950 kernels (rq_kernels.hip, hipcc). Plain-old-data only, passed by
 // value as the single kernel argument.
 //
-// Device weight layout ("RQ layout"). A weight of n rows and k columns has
-// U = k/32 units (32 consecutive elements of a row) per row and SB = k/256
-// super-blocks for the K-quants. It lives in up to four planes, each a
-// row-major array with its own row stride in bytes:
+// Device weight layout ("tiled super-blocks"). Every format is handled in
+// super-blocks of 256 consecutive elements of a row (Q8_0 and Q4_0: eight
+// GGUF blocks; a row's last super-block may be partial, its missing blocks
+// stored as zeros). A row has S = ceil(k / 256) super-blocks. A tile is R
+// rows x S super-blocks, R = 64 / S when S is a power of two <= 32 and 1
+// otherwise; tile t holds rows [R t, R t + R) (rows past n are zeros). In a
+// tile, super-block s of row r occupies slot a = (r - R t) * S + s, and one
+// wave lane serves one slot. Each super-block is cut into C chunks of 16
+// bytes; the main plane stores chunk c of every slot of tile t contiguously,
+//     main + ((t * C + c) * R * S + a) * 16,
+// so each of a wave's chunk loads is one contiguous run of 16 B per lane.
 //
-//   Q4_0  p0: 16 B per unit, byte b = q[b] | q[b+16] << 4 (GGUF's own order)
-//         p1: f16 d per unit
-//   Q8_0  p0: int8 codes, a row = [bytes 0..15 of every unit][bytes 16..31 of
-//             every unit], so each lane's two 16-byte loads are both
-//             contiguous across the wave
-//         p1: f16 d per unit
-//   Q4_K  p0: 16 B per unit (sub-block), byte b = q[b] | q[b+16] << 4
-//         p1: 16 B per super-block, GGUF's d, dmin and packed 6-bit
-//             scales/mins verbatim (unpacked in registers)
-//   Q6_K  p0: 16 B per unit, low nibbles, byte b = lo(q[b]) | lo(q[b+16]) << 4
-//         p1: 8 B per unit, high 2-bit pairs: dword h (elements 16h..16h+15)
-//             holds element 16h+4c+i's bits at bit 8i + 2c (c, i < 4)
-//         p2: the unit's two int8 sub-scales (elements 0-15, 16-31)
-//         p3: f16 d per super-block
+//   Q4_K  C = 9   c0: GGUF d, dmin and packed 6-bit scales/mins, verbatim
+//                 c1+j: sub-block j (32 elements), byte b = q[b] | q[b+16] << 4
+//   Q4_0  C = 9   c0: the eight blocks' f16 d
+//                 c1+j: block j's 16 bytes in GGUF order (same nibble rule)
+//   Q8_0  C = 17  c0: the eight blocks' f16 d
+//                 c1+2j+h: block j's codes 16h .. 16h+15
+//   Q6_K  C = 13  c0: the 16 int8 sub-scales (GGUF bytes 192..207)
+//                 c1+j: sub-block j low nibbles, byte b = lo(q[b]) | lo(q[b+16]) << 4
+//                 c9+i: high 2-bit pairs of sub-blocks 2i, 2i+1, four dwords
+//                       H(2i,0) H(2i,1) H(2i+1,0) H(2i+1,1); H(j,h) holds
+//                       element 32j+16h+4c+e's two bits at bit 8e + 2c
+//         tail plane: f16 d per slot, tail + (t * R * S + a) * 2
 //
-// Every format keeps GGUF's byte count (18/34/144/210 bytes per block): the
-// repack only moves bytes, it adds none and rounds nothing.
+// Byte count per super-block equals GGUF's (144, 144, 272, 210): the repack
+// only moves bytes and rounds nothing.
 #pragma once
 
 #include <stdint.h>
@@ -34,28 +39,31 @@
 #define RQ_FMT_Q6_K 3
 #define RQ_NUM_FMTS 4
 
-// Threads per matvec workgroup (4 waves of 64).
-#define RQ_MV_THREADS 256
-#define RQ_MV_WAVES (RQ_MV_THREADS / 64)
+// Chunks of 16 bytes per super-block, by format.
+static inline int rq_chunks(int fmt) { return fmt == RQ_FMT_Q8_0 ? 17 : (fmt == RQ_FMT_Q6_K ? 13 : 9); }
+
+// Threads per workgroup of every kernel.
+#define RQ_THREADS 256
+#define RQ_WAVES (RQ_THREADS / 64)
 // Weights sharing one activation in one launch (Q/K/V, gate/up).
 #define RQ_MV_TARGETS 3
 // Most activation columns per matvec launch.
 #define RQ_MV_MAX_NC 8
 
-// Rows each wave streams, by activation column count (compile-time in the
-// kernels, mirrored here for the host's grid sizing).
-static inline int rq_mv_rows_per_wave(int nc) { return nc <= 2 ? 4 : (nc <= 4 ? 2 : 1); }
-
-struct RqPlanes {
-    const uint8_t* p[4];
-    int64_t stride[4];
+struct RqTiled {
+    const uint8_t* main;  // chunk plane
+    const uint8_t* tail;  // Q6_K: f16 d per slot; otherwise unused
+    int32_t S;            // super-blocks per row
+    int32_t R;            // rows per tile
+    int32_t T;            // tiles
+    int32_t k;            // columns
 };
 
 struct RqMvTarget {
-    RqPlanes w;
-    float* out;       // out[j * n + r]
-    int32_t n;        // rows
-    int32_t wave_start;  // first global wave index of this target
+    RqTiled w;
+    float* out;          // out[j * n + r]
+    int32_t n;           // rows
+    int32_t wave_start;  // first global wave of this target (one wave per tile)
 };
 
 struct RqMvParams {
@@ -63,9 +71,8 @@ struct RqMvParams {
     const int8_t* xq;    // Q8_1 codes, column j at xq + j * k
     const uint16_t* xd;  // Q8_1 f16 scales, column j at xd + j * k / 32
     int32_t count;
-    int32_t k;
-    int32_t m;  // columns in this launch (<= the kernel's NC)
-    int32_t pad;
+    int32_t m;           // columns in this launch
+    int32_t pad[2];
 };
 
 struct RqQuantParams {
@@ -78,20 +85,19 @@ struct RqQuantParams {
 
 struct RqRepackParams {
     const uint8_t* raw;  // GGUF bytes of rows [row0, row0 + rows)
-    uint8_t* p[4];
-    int64_t stride[4];
+    uint8_t* main;
+    uint8_t* tail;
     int64_t row0;
     int64_t rows;
-    int32_t k;
-    int32_t pad;
+    int32_t S, R, k, pad;
 };
 
 struct RqDotsParams {
-    RqPlanes w;
+    RqTiled w;
     const int8_t* xq;
     const uint16_t* xd;
-    int32_t* dots;
+    int32_t* dots;  // dots[(j * n + r) * nb + b], nb = k/32 (Q6_K: k/16)
     int64_t n;
-    int32_t k;
     int32_t m;
+    int32_t pad;
 };
