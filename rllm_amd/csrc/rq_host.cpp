@@ -94,8 +94,8 @@ constexpr size_t kPlaneAlign = 256;
 constexpr size_t kUploadChunkBytes = size_t(64) << 20;  // as UPLOAD_CHUNK_BYTES, backend.rs:110
 // LDS the batched matvec may stage activations in, per workgroup.
 constexpr int kLdsBudget = 64 << 10;
-// LDS bytes per activation column per super-block column (rq_kernels.hip lds_col).
-constexpr int kLdsPerSb = 384;
+// LDS bytes per activation column per super-block column (RQ_LDS_REC in rq_kernels.hip).
+constexpr int kLdsPerSb = 400;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

@@ -76,7 +76,13 @@ __device__ __forceinline__ bool group_leader(int lane, int g) {
 // v_dot4_i32_i8: c + sum of the four signed byte products.
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-__device__ __forceinline__ int4 ld16(const u8* p) { return *(const int4*)p; }
+// Streaming 16-byte load: weights are read once, so the nontemporal hint
+// keeps them from displacing reusable lines (activations) in the caches.
+__device__ __forceinline__ int4 ld16_nt(const u8* p) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = __builtin_nontemporal_load((const v4i*)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
 
 // ---------------------------------------------------------------------------
 // Q8_1 activations. Eight lanes per 32-value block, four values each (one
@@ -148,7 +154,7 @@ __device__ __forceinline__ void load_sb(const RqTiled& w, int t, int a, SB<FMT>&
     const int64_t slots = (int64_t)w.R * w.S;
     const u8* base = w.main + ((int64_t)t * C * slots + a) * 16;
 #pragma unroll
-    for (int c = 0; c < C; c++) o.c[c] = ld16(base + (int64_t)c * slots * 16);
+    for (int c = 0; c < C; c++) o.c[c] = ld16_nt(base + (int64_t)c * slots * 16);
     o.tail = FMT == RQ_FMT_Q6_K ? (u32) * (const u16*)(w.tail + ((int64_t)t * slots + a) * 2) : 0u;
 }
 
@@ -354,44 +360,38 @@ __device__ __forceinline__ void tile_store(const RqMvTarget& T, int t, int lane,
 // its super-block column's blocks from LDS. A lane walks slots lane, lane +
 // 64, ... of the tile (several passes only when S > 64).
 //
-// LDS per column (384 bytes per super-block column): codes [j][half][s] x
-// 16 B (lanes with consecutive s read consecutive 16 B; lanes of other rows
-// of the tile read the same addresses), then dx, f, ia, ib as [j][s] words.
+// LDS per column: one record of RQ_LDS_REC bytes per super-block column s:
+// the eight blocks' codes (8 x 32 B), then per block {dx, f, ia, ib} (8 x
+// 16 B). Records are 400 B apart (100 dwords), so 16-byte reads by lanes
+// with consecutive s fall in distinct banks, and a lane reads its record at
+// fixed offsets from one base address.
 
-struct LdsX {
-    int4* codes;
-    float* dx;
-    float* f;
-    int* ia;
-    int* ib;
+#define RQ_LDS_REC 400
+
+struct XMeta {
+    float dx, f;
+    int ia, ib;
 };
 
-__device__ __forceinline__ LdsX lds_col(char* base, int S, int col) {
-    char* p = base + (size_t)col * 384 * S;
-    LdsX l;
-    l.codes = (int4*)p;
-    l.dx = (float*)(p + 256 * S);
-    l.f = l.dx + 8 * S;
-    l.ia = (int*)(l.f + 8 * S);
-    l.ib = l.ia + 8 * S;
-    return l;
+__device__ __forceinline__ char* lds_rec(char* base, int S, int col, int s) {
+    return base + ((size_t)col * S + s) * RQ_LDS_REC;
 }
 
-template <int FMT>
-__device__ __forceinline__ void lds_read_x(const LdsX& l, int S, int s, int j, XJ& x) {
-    const int4 lo = l.codes[(2 * j) * S + s], hi = l.codes[(2 * j + 1) * S + s];
+__device__ __forceinline__ void lds_read_x(const char* rec, int j, XJ& x) {
+    const int4 lo = *(const int4*)(rec + 32 * j), hi = *(const int4*)(rec + 32 * j + 16);
+    const XMeta m = *(const XMeta*)(rec + 256 + 16 * j);
     x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
     x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
-    x.dx = l.dx[j * S + s];
-    x.f = FMT == RQ_FMT_Q4_K ? l.f[j * S + s] : 0.f;
-    x.ia = (FMT == RQ_FMT_Q4_0 || FMT == RQ_FMT_Q6_K) ? l.ia[j * S + s] : 0;
-    x.ib = FMT == RQ_FMT_Q6_K ? l.ib[j * S + s] : 0;
+    x.dx = m.dx;
+    x.f = m.f;
+    x.ia = m.ia;
+    x.ib = m.ib;
 }
 
 extern __shared__ char rq_lds[];
 
-// Staging: item it = (col, j, s) is one 32-value block; each thread stages
-// items threadIdx.x + RQ_THREADS * i, two per round.
+// Staging: item it = (col, s, j) is one 32-value block; each thread stages
+// items threadIdx.x + RQ_THREADS * i (consecutive threads fill one record).
 struct StageItem {
     int col, j, s, b;
     bool store, valid;
@@ -403,8 +403,8 @@ __device__ __forceinline__ StageItem stage_item(int it, int total, int S, int U)
     const int itc = si.store ? it : total - 1;
     si.col = itc / (8 * S);
     const int rem = itc % (8 * S);
-    si.j = rem / S;
-    si.s = rem % S;
+    si.s = rem >> 3;
+    si.j = rem & 7;
     si.b = 8 * si.s + si.j;
     si.valid = si.b < U;
     return si;
@@ -414,13 +414,15 @@ template <int FMT>
 __device__ __forceinline__ void stage_write(const StageItem& si, XJ& x, int S) {
     prep_x<FMT>(x, si.valid);
     if (si.store) {
-        const LdsX l = lds_col(rq_lds, S, si.col);
-        l.codes[(2 * si.j) * S + si.s] = make_int4(x.q[0], x.q[1], x.q[2], x.q[3]);
-        l.codes[(2 * si.j + 1) * S + si.s] = make_int4(x.q[4], x.q[5], x.q[6], x.q[7]);
-        l.dx[si.j * S + si.s] = x.dx;
-        l.f[si.j * S + si.s] = x.f;
-        l.ia[si.j * S + si.s] = x.ia;
-        l.ib[si.j * S + si.s] = x.ib;
+        char* rec = lds_rec(rq_lds, S, si.col, si.s);
+        *(int4*)(rec + 32 * si.j) = make_int4(x.q[0], x.q[1], x.q[2], x.q[3]);
+        *(int4*)(rec + 32 * si.j + 16) = make_int4(x.q[4], x.q[5], x.q[6], x.q[7]);
+        XMeta m;
+        m.dx = x.dx;
+        m.f = x.f;
+        m.ia = x.ia;
+        m.ib = x.ib;
+        *(XMeta*)(rec + 256 + 16 * si.j) = m;
     }
 }
 
@@ -430,12 +432,12 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
     const SBScale sc = sb_scale<FMT>(w);
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-        const LdsX l = lds_col(rq_lds, S, c);
+        const char* rec = lds_rec(rq_lds, S, c, s);
         float accd = 0.f, accm = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             XJ x;
-            lds_read_x<FMT>(l, S, s, j, x);
+            lds_read_x(rec, j, x);
             int s0, s1;
             sub_dot<FMT>(w, j, x, s0, s1);
             sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
