@@ -188,7 +188,71 @@ def cpu_baseline(orc, t, n, k, reps=5):
             "sample": f"Q4_K {n}x{k} m=1 matvec, {reps} timed runs after one warm-up (median {med * 1e3:.1f} ms)"}
 
 
+COPY_BYTES = 64 << 20
+KERNEL = "rq_mvx_q4_k_1"
+
+
+def traffic_child() -> int:
+    """Run under rocprofv3 --pmc: a 64 MiB device copy (counter calibration), then 64 Q4_K matvec launches."""
+    import torch
+
+    from oracle import oracle as orc
+    from rllm_amd.backend import HipBackend, HostTensor
+    from rllm_amd.dtype import DType
+
+    gpu = HipBackend(0)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=gpu.device).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    T, N, K = 12, 14336, 4096
+    w = gpu.upload(HostTensor("w", DType(T), (N, K), make_gguf(orc, T, N, K, 7)))
+    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(8, K)), 1, K)
+    out = gpu.alloc(N)
+    for _ in range(64):
+        gpu.matvec(xq, w, out, 1)
+    torch.cuda.synchronize()
+    gpu.close()
+    return 0
+
+
+def measure_traffic() -> dict | None:
+    """HBM bytes per launch of the Q4_K matvec from two rocprofv3 --pmc passes
+    (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter reads
+    for a plain 64 MiB device-to-device copy. Runs before this process touches
+    the GPU; returns None if rocprofv3 or the counters are unavailable."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    if not shutil.which("rocprofv3"):
+        return None
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory() as d:
+            cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d,
+                   "-o", "run", "--", sys.executable, os.path.abspath(__file__), "--traffic-child"]
+            r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, cwd=d)
+            files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs if f.endswith("counter_collection.csv")]
+            if r.returncode != 0 or not files:
+                log(f"traffic: rocprofv3 --pmc {counter} failed ({r.returncode}): {r.stdout[-500:]}")
+                return None
+            rows = list(csv.DictReader(open(files[0])))
+        copy = [float(x["Counter_Value"]) for x in rows if "copyBuffer" in x["Kernel_Name"]]
+        kern = [float(x["Counter_Value"]) for x in rows if x["Kernel_Name"] == KERNEL]
+        if not copy or not kern:
+            return None
+        scale = (COPY_BYTES / 1024) / max(copy)  # KiB the copy moves / KiB the counter reports
+        res[counter] = statistics.median(kern) * scale * 1024
+        res[counter + "_scale"] = scale
+    return {"bytes": res["FETCH_SIZE"] + res["WRITE_SIZE"], "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
+            "fetch_scale": res["FETCH_SIZE_scale"], "write_scale": res["WRITE_SIZE_scale"]}
+
+
 def main() -> int:
+    if "--traffic-child" in sys.argv:
+        return traffic_child()
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4096, help="timed matvec launches")
@@ -197,11 +261,18 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all-configs", action="store_true", help="also time every BASELINE config (stderr)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run a 64 MiB device-to-device copy (the reference kernel for HBM counter scaling)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the matvec path has no "
               "multi-GPU code; see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
+    traffic = None if args.no_traffic else measure_traffic()
+    if traffic:
+        log(f"traffic: {traffic['bytes'] / 1e6:.2f} MB per launch (fetch x{traffic['fetch_scale']:.4f}, "
+            f"write x{traffic['write_scale']:.4f})")
 
     import torch
 
@@ -210,6 +281,13 @@ def main() -> int:
 
     gpu = HipBackend(0)
     log(f"device: {gpu.name()}, {gpu.compute_units} CUs")
+    if args.calibrate:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=gpu.device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     T, N, K = 12, 14336, 4096
     r = bench_matvec(torch, gpu, orc, T, N, K, 1, args.steps, args.warmup)
     log(f"Q4_K {N}x{K} m=1: {r['us']:.2f} us/launch, {r['gbs']:.0f} GB/s "
@@ -253,8 +331,9 @@ def main() -> int:
         "decode_tok_s": round(dec["tok_s"], 1) if dec else None,
         "decode_step_us": round(dec["us"], 1) if dec else None,
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rq_mv_q4_k_1", "kernel_us": round(r["us"], 3), "alg_bytes": r["bytes"]},
+                     "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic["bytes"]) if traffic else None,
+                     "kernel": KERNEL, "kernel_us": round(r["us"], 3), "alg_bytes": r["bytes"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
