@@ -143,7 +143,6 @@ def bench_decode(torch, gpu, orc, replays):
     xf = gpu.from_host(orc.normal(6, 14336))
     bufs = {name: gpu.alloc(n) for name, t, n, k in LAYER}
     logits = gpu.alloc(HEAD[2])
-    gpu.reserve(14336)
 
     def step():
         for L in layers:

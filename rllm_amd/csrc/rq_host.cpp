@@ -92,7 +92,9 @@ const char* const kFmtSuffix[RQ_NUM_FMTS] = {"q4_0", "q8_0", "q4_k", "q6_k"};
 
 constexpr size_t kPlaneAlign = 256;
 constexpr size_t kUploadChunkBytes = size_t(64) << 20;  // as UPLOAD_CHUNK_BYTES, backend.rs:110
-// LDS the batched matvec may stage activations in, per workgroup.
+// LDS a 256-thread matvec workgroup may stage activations in (two such
+// workgroups share a CU's LDS). The 1024-thread workgroups, one per CU, may
+// use what the device allows a workgroup (rq_ctx::lds_wide).
 constexpr int kLdsBudget = 64 << 10;
 // LDS bytes per activation column per super-block column (RQ_LDS_REC in rq_kernels.hip).
 constexpr int kLdsPerSb = 400;
@@ -109,16 +111,19 @@ struct rq_ctx {
     char arch[64] = {0};
     hipModule_t mod = nullptr;
     hipFunction_t quant = nullptr;
-    hipFunction_t mvx[RQ_NUM_FMTS][RQ_MV_MAX_NC + 1] = {};
-    hipFunction_t dots[RQ_NUM_FMTS] = {};
-    hipFunction_t repack[RQ_NUM_FMTS] = {};
-    hipStream_t stream = nullptr;
-    // Q8_1 scratch for rq_matmul / rq_matmul_many (grown on demand, or
-    // sized up front by rq_reserve).
+    int lds_wide = 0;  // LDS bytes a wide matvec workgroup may use
+    // [0]: 256-thread workgroups, [1]: RQ_MV_WIDE_THREADS(fmt)-thread workgroups.
+    hipFunction_t mvx[2][RQ_NUM_FMTS][RQ_MV_MAX_NC + 1] = {};  // Q8_1 activations
+    hipFunction_t mvf[2][RQ_NUM_FMTS] = {};                    // one f32 column, quantized while staging
+    // Q8_1 scratch of rq_matmul / rq_matmul_many for m >= 2 (grown on
+    // demand, or sized up front by rq_reserve).
     int8_t* sq = nullptr;
     uint16_t* sd = nullptr;
     uint16_t* ss = nullptr;
     int64_t scap = 0;
+    hipFunction_t dots[RQ_NUM_FMTS] = {};
+    hipFunction_t repack[RQ_NUM_FMTS] = {};
+    hipStream_t stream = nullptr;
 };
 
 struct rq_weight {
@@ -140,13 +145,13 @@ rq_status bind(rq_ctx* ctx) {
 }
 
 rq_status launch(rq_ctx* ctx, hipFunction_t f, const char* name, uint64_t grid, const void* params,
-                 unsigned lds = 0) {
+                 unsigned lds = 0, unsigned threads = RQ_THREADS) {
     if (grid == 0) return RQ_OK;
     if (grid > 0x7fffffffull)
         return fail(RQ_ERR_SHAPE, "%s: grid of %llu workgroups too large", name, (unsigned long long)grid);
     // One by-value argument: the parameter block.
     void* args[] = {const_cast<void*>(params)};
-    hipError_t e = hipModuleLaunchKernel(f, (unsigned)grid, 1, 1, RQ_THREADS, 1, 1, lds, ctx->stream, args, nullptr);
+    hipError_t e = hipModuleLaunchKernel(f, (unsigned)grid, 1, 1, threads, 1, 1, lds, ctx->stream, args, nullptr);
     if (e != hipSuccess)
         return fail(RQ_ERR_BACKEND, "hipModuleLaunchKernel(%s): %s (%d)", name, hipGetErrorName(e), (int)e);
     return RQ_OK;
@@ -170,21 +175,36 @@ void tile_geometry(int64_t rows, int64_t cols, RqTiled& t) {
     t.T = (int32_t)((rows + t.R - 1) / t.R);
 }
 
-// Most activation columns the LDS-staged matvec can take for S super-blocks.
-int mvx_max_cols(int S) { return std::max(0, std::min(RQ_MV_MAX_NC, kLdsBudget / (kLdsPerSb * S))); }
+// Most activation columns a matvec workgroup can stage for S super-blocks
+// within `budget` bytes of LDS.
+int mvx_max_cols(int S, int budget) { return std::max(0, std::min(RQ_MV_MAX_NC, budget / (kLdsPerSb * S))); }
 
-// One matvec launch per group of columns (as many as the LDS staging
-// budget allows, at most RQ_MV_MAX_NC), over `count` same-type weights of
-// width k; one wave per tile.
-rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, int64_t m, const rq_weight* const* ws,
-                        float* const* outs, int count) {
+// Workgroup width for tiles of R rows: RQ_MV_WIDE_THREADS (16 tiles; Q8_0: 8)
+// when a tile holds fewer than 4 rows and the staging is heavy enough to be
+// worth sharing across 16 rows rather than 4 (f32 activations, quantized while
+// staging, or two or more Q8_1 columns); otherwise 256 threads (4 tiles).
+// Measured on MI355X at k = 14336 (S = 56, R = 1): one Q8_1 column runs
+// faster in 256-thread workgroups, every other case in 1024-thread ones.
+bool mv_wide(int R, int64_t m, bool f32_in) { return R < 4 && (f32_in || m >= 2); }
+
+// Matvec launches over `count` same-type weights of width k, one wave per
+// tile. The m activation columns are split into the fewest groups the LDS
+// staging allows (at most RQ_MV_MAX_NC columns each), of near-equal size;
+// every launch reads the weights once. Activations are Q8_1 (xq, xd) or,
+// when xf is set, f32 quantized by the kernel while it stages them
+// (rq_mvf_*, rq_mvfw_*).
+rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
+                        const rq_weight* const* ws, float* const* outs, int count) {
     const int fmt = ws[0]->fmt;
     const int64_t k = ws[0]->cols, U = (k + 31) / 32;
     const int S = ws[0]->tiled.S;
-    const int group = mvx_max_cols(S);
+    const int wide = mv_wide(ws[0]->tiled.R, m, xf != nullptr) ? 1 : 0;
+    const int waves_per_wg = wide ? RQ_MV_WIDE_THREADS(fmt) / 64 : RQ_WAVES;
+    const int group = mvx_max_cols(S, wide ? ctx->lds_wide : kLdsBudget);
     if (group < 1) return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage", (long long)k);
-    for (int64_t g0 = 0; g0 < m; g0 += group) {
-        const int nc = (int)std::min<int64_t>(group, m - g0);
+    const int64_t ngroups = (m + group - 1) / group;
+    for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
+        const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
         RqMvParams p;
         memset(&p, 0, sizeof p);
         int64_t waves = 0;
@@ -196,17 +216,25 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, int64
             p.t[i].wave_start = (int32_t)waves;
             waves += w->tiled.T;
         }
-        p.xq = xq + g0 * k;
-        p.xd = xd + g0 * U;
+        if (xf) {
+            p.xf = xf + g0 * k;
+        } else {
+            p.xq = xq + g0 * k;
+            p.xd = xd + g0 * U;
+        }
         p.count = count;
         p.m = nc;
-        const uint64_t blocks = (uint64_t)((waves + RQ_WAVES - 1) / RQ_WAVES);
-        rq_status st = launch(ctx, ctx->mvx[fmt][nc], "rq_mvx", blocks, &p, (unsigned)(nc * kLdsPerSb * S));
+        const uint64_t blocks = (uint64_t)((waves + waves_per_wg - 1) / waves_per_wg);
+        rq_status st = launch(ctx, xf ? ctx->mvf[wide][fmt] : ctx->mvx[wide][fmt][nc], xf ? "rq_mvf" : "rq_mvx",
+                              blocks, &p, (unsigned)(nc * kLdsPerSb * S), (unsigned)(64 * waves_per_wg));
         if (st != RQ_OK) return st;
+        g0 += nc;
     }
     return RQ_OK;
 }
 
+// Grows the Q8_1 scratch to `values` elements. Refuses while the stream is
+// being captured (an allocation there would not be replayed).
 rq_status ensure_scratch(rq_ctx* ctx, int64_t values) {
     if (values <= ctx->scap) return RQ_OK;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -258,7 +286,8 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     hipDeviceProp_t prop;
     if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return bail(hip_fail("hipGetDeviceProperties", e));
     ctx->cus = prop.multiProcessorCount;
-    snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
+    ctx->lds_wide = (int)std::min<size_t>(prop.sharedMemPerBlock, size_t(160) << 10);
+    snprintf(ctx->arch, sizeof ctx->arch, "%.63s", prop.gcnArchName);
     if (strncmp(ctx->arch, "gfx950", 6) != 0)
         return bail(fail(RQ_ERR_UNSUPPORTED, "rq_open: device %d is %s; librq is built for gfx950 only", device, ctx->arch));
     if ((e = hipModuleLoadData(&ctx->mod, rq_kernels_blob)) != hipSuccess) return bail(hip_fail("hipModuleLoadData", e));
@@ -272,8 +301,14 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     char name[64];
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
         for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {
-            snprintf(name, sizeof name, "rq_mvx_%s_%d", kFmtSuffix[f], nc);
-            st = get(&ctx->mvx[f][nc], name);
+            for (int wide = 0; wide < 2 && st == RQ_OK; wide++) {
+                snprintf(name, sizeof name, "rq_mvx%s_%s_%d", wide ? "w" : "", kFmtSuffix[f], nc);
+                st = get(&ctx->mvx[wide][f][nc], name);
+            }
+        }
+        for (int wide = 0; wide < 2 && st == RQ_OK; wide++) {
+            snprintf(name, sizeof name, "rq_mvf%s_%s", wide ? "w" : "", kFmtSuffix[f]);
+            st = get(&ctx->mvf[wide][f], name);
         }
         if (st != RQ_OK) break;
         snprintf(name, sizeof name, "rq_dots_%s", kFmtSuffix[f]);
@@ -525,7 +560,7 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if ((st = check_len("matmul out", out_lens[i], m * ws[i]->rows)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
-    return matvec_launch(ctx, xq->qs, xq->d, m, ws, outs, count);
+    return matvec_launch(ctx, xq->qs, xq->d, nullptr, m, ws, outs, count);
 }
 
 extern "C" rq_status rq_matvec(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* w, float* out,
@@ -564,17 +599,27 @@ extern "C" rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, 
     for (int i = 0; i < count; i++)
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matmul: output %d not 4-byte aligned", i);
     if ((st = bind(ctx)) != RQ_OK) return st;
-    // Quantize x once, then one launch per run of <= 3 same-type weights.
-    if ((st = ensure_scratch(ctx, m * k)) != RQ_OK) return st;
-    RqQuantParams qp{x, ctx->sq, ctx->sd, ctx->ss, m * k / 32};
-    if ((st = launch(ctx, ctx->quant, "rq_quantize_q8_1", (uint64_t)((qp.nblocks * 8 + RQ_THREADS - 1) / RQ_THREADS),
-                     &qp)) != RQ_OK)
-        return st;
+    // m == 1: each launch quantizes x while staging it (bit-identical to
+    // rq_quantize_q8_1), saving the quantize launch. For m >= 2 the staging
+    // of f32 columns costs every workgroup more than the launch saves
+    // (4 B per value read, and the rounding, per workgroup, against 1.125 B
+    // of Q8_1), so x is quantized once into the scratch instead.
+    const bool fused = m == 1;
+    if (!fused) {
+        if ((st = ensure_scratch(ctx, m * k)) != RQ_OK) return st;
+        RqQuantParams qp{x, ctx->sq, ctx->sd, ctx->ss, m * k / 32};
+        if ((st = launch(ctx, ctx->quant, "rq_quantize_q8_1",
+                         (uint64_t)((qp.nblocks * 8 + RQ_THREADS - 1) / RQ_THREADS), &qp)) != RQ_OK)
+            return st;
+    }
+    // One launch per run of <= 3 same-type weights.
     int i = 0;
     while (i < count) {
         int g = 1;
         while (g < RQ_MV_TARGETS && i + g < count && ws[i + g]->type == ws[i]->type) g++;
-        if ((st = matvec_launch(ctx, ctx->sq, ctx->sd, m, ws + i, outs + i, g)) != RQ_OK) return st;
+        st = fused ? matvec_launch(ctx, nullptr, nullptr, x, m, ws + i, outs + i, g)
+                   : matvec_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, outs + i, g);
+        if (st != RQ_OK) return st;
         i += g;
     }
     return RQ_OK;

@@ -7,7 +7,9 @@
 //
 //   rq_quantize_q8_1     f32 activations -> Q8_1 (int8 + f16 d + f16 s per 32)
 //   rq_repack_<fmt>      GGUF blocks -> tiled super-blocks (upload path)
-//   rq_mvx_<fmt>_<nc>    matvec over nc = 1..8 activation columns (staged in LDS)
+//   rq_mvx_<fmt>_<nc>    matvec over nc = 1..8 Q8_1 activation columns (staged in LDS)
+//   rq_mvf_<fmt>         one f32 activation column, quantized while staging
+//   rq_mvxw_*, rq_mvfw_* the same with 1024-thread (Q8_0: 512) workgroups (tiles of < 4 rows)
 //   rq_dots_<fmt>        the int32 block dots of the matvecs, written out (debug)
 //
 // Mapping: one lane per super-block (256 elements) of a row, R rows per
@@ -94,6 +96,38 @@ __device__ __forceinline__ int4 ld16_nt(const u8* p) {
 // are IEEE divisions (built with -fhip-fp32-correctly-rounded-divide-sqrt),
 // rintf rounds half to even, f16 conversion rounds to nearest even.
 
+// Codes q_i = rint(x_i / d) of n values of one block, d = amax / 127 with
+// amax >= |x_i|: the IEEE quotient rounded half to even, without dividing
+// per value where that is provably unnecessary.
+//
+// Fast path: r = 1 / d (IEEE) and t = x * r. Each rounding is a relative
+// error of at most 2^-24, and |x / d| <= 190.5 (127 (1 + 2^-23) unless d is
+// subnormal, where d = RN(amax / 127) can undershoot by up to a third), so
+// |t - x / d| <= 190.5 * (2^-23 + 2^-48) < 2.3e-5 (t is subnormal only when
+// x / d is far below 1/2, where both round to 0). When t lies farther than
+// 2^-14 (6.1e-5) from every half-integer, x / d falls strictly inside the same
+// rounding interval and rint(x / d) = rint(t). A lane any of whose values
+// misses that window recomputes all of them with the division; so do d = 0
+// (r infinite, t NaN) and infinite or NaN inputs, where the window test is
+// false. The codes are therefore the division's in every case.
+template <int N>
+__device__ __forceinline__ void q8_codes(const float* x, float d, int* q) {
+#pragma clang fp contract(off)
+    const float r = 1.0f / d;
+    bool near_tie = false;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float t = x[i] * r;
+        const float rt = rintf(t);
+        near_tie |= !(fabsf(t - rt) < 0.49993896484375f);  // 0.5 - 2^-14
+        q[i] = (int)rt;
+    }
+    if (near_tie) {
+#pragma unroll
+        for (int i = 0; i < N; i++) q[i] = d > 0.f ? (int)rintf(x[i] / d) : 0;
+    }
+}
+
 extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_quantize_q8_1(RqQuantParams p) {
     const int64_t t = (int64_t)blockIdx.x * RQ_THREADS + threadIdx.x;
     const int64_t blk = t >> 3;
@@ -104,12 +138,11 @@ extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_quantize_q8_1(RqQuan
     amax = fmaxf(amax, dpp_f<DPP_QUAD_2301>(amax));
     amax = fmaxf(amax, dpp_f<DPP_ROW_HALF_MIRROR>(amax));
     const float d = amax / 127.0f;
-    const int q0 = d > 0.f ? (int)rintf(v.x / d) : 0;
-    const int q1 = d > 0.f ? (int)rintf(v.y / d) : 0;
-    const int q2 = d > 0.f ? (int)rintf(v.z / d) : 0;
-    const int q3 = d > 0.f ? (int)rintf(v.w / d) : 0;
-    ((int*)p.qs)[t] = (q0 & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | ((q3 & 0xFF) << 24);
-    int sum = q0 + q1 + q2 + q3;
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    int q[4];
+    q8_codes<4>(xv, d, q);
+    ((int*)p.qs)[t] = (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | ((q[3] & 0xFF) << 24);
+    int sum = q[0] + q[1] + q[2] + q[3];
     sum += dpp_i<DPP_QUAD_1032>(sum);
     sum += dpp_i<DPP_QUAD_2301>(sum);
     sum += dpp_i<DPP_ROW_HALF_MIRROR>(sum);
@@ -390,8 +423,9 @@ __device__ __forceinline__ void lds_read_x(const char* rec, int j, XJ& x) {
 
 extern __shared__ char rq_lds[];
 
-// Staging: item it = (col, s, j) is one 32-value block; each thread stages
-// items threadIdx.x + RQ_THREADS * i (consecutive threads fill one record).
+// Staging: item it = (col, s, j) is one 32-value block; each thread of a
+// workgroup of n threads stages items threadIdx.x + n * i (consecutive
+// threads fill one record).
 struct StageItem {
     int col, j, s, b;
     bool store, valid;
@@ -426,6 +460,65 @@ __device__ __forceinline__ void stage_write(const StageItem& si, XJ& x, int S) {
     }
 }
 
+// Staging from f32 activations (the fused quantize of rq_matmul): four lanes
+// (a quad) per 32-value block, eight values each; amax and the code sums meet
+// across the quad with DPP. The arithmetic is rq_quantize_q8_1's (q8_codes,
+// f16 rounding of d), so the staged codes and scales are bit-identical to a
+// separate quantize launch. A workgroup of n threads stages n / 4 items per
+// round.
+
+struct QItem {
+    StageItem si;
+    float v[8];
+};
+
+__device__ __forceinline__ void qitem_load(const float* __restrict__ xf, int k, int total, int S, int U, int base,
+                                           QItem& q) {
+    q.si = stage_item(base + (threadIdx.x >> 2), total, S, U);
+    const float4* p = (const float4*)(xf + (int64_t)q.si.col * k + (int64_t)(q.si.valid ? q.si.b : 0) * 32 +
+                                      8 * (threadIdx.x & 3));
+    const float4 a = p[0], b = p[1];
+    q.v[0] = a.x; q.v[1] = a.y; q.v[2] = a.z; q.v[3] = a.w;
+    q.v[4] = b.x; q.v[5] = b.y; q.v[6] = b.z; q.v[7] = b.w;
+}
+
+// All lanes of the wave must be active (quad DPP).
+template <int FMT>
+__device__ __forceinline__ void qitem_write(QItem& q, int S) {
+    const int ql = threadIdx.x & 3;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        if (!q.si.valid) q.v[i] = 0.f;
+        amax = fmaxf(amax, fabsf(q.v[i]));
+    }
+    amax = fmaxf(amax, dpp_f<DPP_QUAD_1032>(amax));
+    amax = fmaxf(amax, dpp_f<DPP_QUAD_2301>(amax));
+    const float d = amax / 127.0f;
+    int qv[8], sum = 0;
+    q8_codes<8>(q.v, d, qv);
+#pragma unroll
+    for (int i = 0; i < 8; i++) sum += qv[i];
+    const int pair = sum + dpp_i<DPP_QUAD_1032>(sum);  // lanes 0,1: codes 0..15; lanes 2,3: codes 16..31
+    const int other = dpp_i<DPP_QUAD_2301>(pair);       // lane 0: the sum of codes 16..31
+    if (q.si.store) {
+        char* rec = lds_rec(rq_lds, S, q.si.col, q.si.s);
+        int2 c;
+        c.x = (qv[0] & 0xFF) | ((qv[1] & 0xFF) << 8) | ((qv[2] & 0xFF) << 16) | ((qv[3] & 0xFF) << 24);
+        c.y = (qv[4] & 0xFF) | ((qv[5] & 0xFF) << 8) | ((qv[6] & 0xFF) << 16) | ((qv[7] & 0xFF) << 24);
+        *(int2*)(rec + 32 * q.si.j + 8 * ql) = c;
+        if (ql == 0) {
+            const int sa = pair, sb = other;
+            XMeta m;
+            m.dx = h2f(f2h(d));
+            m.f = FMT == RQ_FMT_Q4_K ? m.dx * (float)(sa + sb) : 0.f;
+            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * (sa + sb) : (FMT == RQ_FMT_Q6_K ? -32 * sa : 0);
+            m.ib = FMT == RQ_FMT_Q6_K ? -32 * sb : 0;
+            *(XMeta*)(rec + 256 + 16 * q.si.j) = m;
+        }
+    }
+}
+
 // Dot of one super-block slot with nc columns, accumulated into acc.
 template <int FMT, int NC>
 __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool active, float* acc) {
@@ -447,10 +540,11 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
     }
 }
 
-template <int FMT, int NC>
+template <int FMT, int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
+    constexpr int THREADS = 64 * WAVES, QITEMS = THREADS / 4;
     const int lane = threadIdx.x & 63;
-    const int gwave = blockIdx.x * RQ_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gwave = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // All targets of one launch share k, so the staged columns serve every wave.
     const int S = P.t[0].w.S, k = P.t[0].w.k, U = (k + 31) >> 5;
     int ti = 0;
@@ -466,21 +560,36 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // valid tile; waves without one discard it), then the LDS writes, which
     // wait only for the staging loads issued before the weights.
     const int total = NC * 8 * S;
-    StageItem si0 = stage_item(threadIdx.x, total, S, U);
-    StageItem si1 = stage_item(threadIdx.x + RQ_THREADS, total, S, U);
-    XJ x0, x1;
-    load_x_raw(P.xq + (int64_t)si0.col * k, P.xd + (int64_t)si0.col * U, si0.valid ? si0.b : 0, x0);
-    load_x_raw(P.xq + (int64_t)si1.col * k, P.xd + (int64_t)si1.col * U, si1.valid ? si1.b : 0, x1);
     SB<FMT> w;
-    load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, a0, w);
-    __builtin_amdgcn_sched_barrier(0);
-    stage_write<FMT>(si0, x0, S);
-    stage_write<FMT>(si1, x1, S);
-    for (int it = threadIdx.x + 2 * RQ_THREADS; it < total; it += RQ_THREADS) {
-        const StageItem si = stage_item(it, total, S, U);
-        XJ x;
-        load_x_raw(P.xq + (int64_t)si.col * k, P.xd + (int64_t)si.col * U, si.valid ? si.b : 0, x);
-        stage_write<FMT>(si, x, S);
+    if (F32IN) {
+        QItem q0, q1;
+        qitem_load(P.xf, k, total, S, U, 0, q0);
+        qitem_load(P.xf, k, total, S, U, QITEMS, q1);
+        load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, a0, w);
+        __builtin_amdgcn_sched_barrier(0);
+        qitem_write<FMT>(q0, S);
+        qitem_write<FMT>(q1, S);
+        for (int base = 2 * QITEMS; base < total; base += QITEMS) {  // uniform trip count
+            QItem q;
+            qitem_load(P.xf, k, total, S, U, base, q);
+            qitem_write<FMT>(q, S);
+        }
+    } else {
+        StageItem si0 = stage_item(threadIdx.x, total, S, U);
+        StageItem si1 = stage_item(threadIdx.x + THREADS, total, S, U);
+        XJ x0, x1;
+        load_x_raw(P.xq + (int64_t)si0.col * k, P.xd + (int64_t)si0.col * U, si0.valid ? si0.b : 0, x0);
+        load_x_raw(P.xq + (int64_t)si1.col * k, P.xd + (int64_t)si1.col * U, si1.valid ? si1.b : 0, x1);
+        load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, a0, w);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_write<FMT>(si0, x0, S);
+        stage_write<FMT>(si1, x1, S);
+        for (int it = threadIdx.x + 2 * THREADS; it < total; it += THREADS) {
+            const StageItem si = stage_item(it, total, S, U);
+            XJ x;
+            load_x_raw(P.xq + (int64_t)si.col * k, P.xd + (int64_t)si.col * U, si.valid ? si.b : 0, x);
+            stage_write<FMT>(si, x, S);
+        }
     }
     __syncthreads();
     if (!has_tile) return;  // wave-uniform; no barrier follows
@@ -502,8 +611,22 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     for (int c = 0; c < NC; c++) tile_store(T, t, lane, rt, g, acc[c], c);
 }
 
-#define RQ_MVX(NAME, FMT, NC) \
-    extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvx_##NAME##_##NC(RqMvParams p) { mvx_body<FMT, NC>(p); }
+#define RQ_MVX(NAME, FMT, NC)                                                                                         \
+    extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvx_##NAME##_##NC(RqMvParams p) {                     \
+        mvx_body<FMT, NC, false, RQ_WAVES>(p);                                                                        \
+    }                                                                                                                 \
+    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvxw_##NAME##_##NC(RqMvParams p) {       \
+        mvx_body<FMT, NC, false, RQ_MV_WIDE_THREADS(FMT) / 64>(p);                                                    \
+    }
+
+// f32 activations: one column (rq_matmul with m == 1).
+#define RQ_MVF(NAME, FMT)                                                                                             \
+    extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvf_##NAME(RqMvParams p) {                            \
+        mvx_body<FMT, 1, true, RQ_WAVES>(p);                                                                          \
+    }                                                                                                                 \
+    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvfw_##NAME(RqMvParams p) {              \
+        mvx_body<FMT, 1, true, RQ_MV_WIDE_THREADS(FMT) / 64>(p);                                                      \
+    }
 
 #define RQ_MVX_ALL(NAME, FMT) \
     RQ_MVX(NAME, FMT, 1)      \
@@ -513,7 +636,8 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     RQ_MVX(NAME, FMT, 5)      \
     RQ_MVX(NAME, FMT, 6)      \
     RQ_MVX(NAME, FMT, 7)      \
-    RQ_MVX(NAME, FMT, 8)
+    RQ_MVX(NAME, FMT, 8)      \
+    RQ_MVF(NAME, FMT)
 
 RQ_MVX_ALL(q4_0, RQ_FMT_Q4_0)
 RQ_MVX_ALL(q8_0, RQ_FMT_Q8_0)

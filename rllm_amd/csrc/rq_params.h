@@ -42,9 +42,16 @@
 // Chunks of 16 bytes per super-block, by format.
 static inline int rq_chunks(int fmt) { return fmt == RQ_FMT_Q8_0 ? 17 : (fmt == RQ_FMT_Q6_K ? 13 : 9); }
 
-// Threads per workgroup of every kernel.
+// Threads per workgroup of every kernel but the wide matvecs.
 #define RQ_THREADS 256
 #define RQ_WAVES (RQ_THREADS / 64)
+// Threads per workgroup of rq_mvxw_* / rq_mvfw_*: weights whose tiles hold
+// fewer than 4 rows (R < 4) stage each activation once per 16 waves rather
+// than per 4, so the staging (and, from f32, the quantization) is shared by
+// as many rows as a 4-row tile's workgroup shares it. Q8_0 holds 17 chunks
+// (68 registers) of weights per lane and does not fit the 128 registers a
+// wave of a 1024-thread workgroup may use, so its wide workgroups have 512.
+#define RQ_MV_WIDE_THREADS(fmt) ((fmt) == RQ_FMT_Q8_0 ? 512 : 1024)
 // Weights sharing one activation in one launch (Q/K/V, gate/up).
 #define RQ_MV_TARGETS 3
 // Most activation columns per matvec launch.
@@ -70,6 +77,7 @@ struct RqMvParams {
     RqMvTarget t[RQ_MV_TARGETS];
     const int8_t* xq;    // Q8_1 codes, column j at xq + j * k
     const uint16_t* xd;  // Q8_1 f16 scales, column j at xd + j * k / 32
+    const float* xf;     // rq_mvf_*: f32 activations, column j at xf + j * k
     int32_t count;
     int32_t m;           // columns in this launch
     int32_t pad[2];
