@@ -107,8 +107,9 @@ def bench_matvec(torch, gpu, orc, t, n, k, m, steps, warmup, seed=7):
     x = orc.normal(seed + 1, m * k, 0.0, 1.0)
     xq = gpu.quantize_q8_1(gpu.from_host(x), m, k)
     out = gpu.alloc(m * n)
-    chunk = min(256, max(copies, 16))
-    chunk = (chunk // copies) * copies if chunk >= copies else copies
+    # Launches per graph: the largest multiple of `copies` up to 256, so that
+    # the graph-launch gap between replays is spread over many kernels.
+    chunk = max(1, 256 // copies) * copies
     replays_w = max(1, warmup // chunk)
     replays = max(1, steps // chunk)
     us, g = time_graph(torch, gpu, lambda i: gpu.matvec(xq, ws[i % copies], out, m), chunk, replays, replays_w)
