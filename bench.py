@@ -104,6 +104,7 @@ def bench_matvec(torch, gpu, orc, t, n, k, m, steps, warmup, seed=7):
         copies = 2
     w = make_gguf(orc, t, n, k, seed, "random" if n * k > 200_000_000 else "normal")
     ws = [gpu.upload(HostTensor(f"w{i}", DType(t), (n, k), w)) for i in range(copies)]
+    family = ws[0].kernels
     x = orc.normal(seed + 1, m * k, 0.0, 1.0)
     xq = gpu.quantize_q8_1(gpu.from_host(x), m, k)
     out = gpu.alloc(m * n)
@@ -123,7 +124,7 @@ def bench_matvec(torch, gpu, orc, t, n, k, m, steps, warmup, seed=7):
     torch.cuda.synchronize()
     b = alg_bytes(t, n, k, m)
     return {"us": us, "gbs": b / us / 1e3, "copies": copies, "launches": replays * chunk, "check_rel": rel,
-            "bytes": b}
+            "bytes": b, "kernels": family}
 
 
 def bench_decode(torch, gpu, orc, replays):
@@ -189,7 +190,13 @@ def cpu_baseline(orc, t, n, k, reps=5):
 
 
 COPY_BYTES = 64 << 20
-KERNEL = "rq_mvx_q4_k_1"
+# Kernel names of the headline matvec (Q4_K, one column) per family: the
+# MFMA kernel's suffix is its super-blocks per wave, picked by the library.
+KERNEL_PREFIX = {"mfma": "rq_mmq_q4_k_1_", "dot4": "rq_mvx_q4_k_1"}
+
+
+def headline_kernel(name: str) -> bool:
+    return name.startswith(KERNEL_PREFIX["mfma"]) or name == KERNEL_PREFIX["dot4"]
 
 
 def traffic_child() -> int:
@@ -240,7 +247,7 @@ def measure_traffic() -> dict | None:
                 return None
             rows = list(csv.DictReader(open(files[0])))
         copy = [float(x["Counter_Value"]) for x in rows if "copyBuffer" in x["Kernel_Name"]]
-        kern = [float(x["Counter_Value"]) for x in rows if x["Kernel_Name"] == KERNEL]
+        kern = [float(x["Counter_Value"]) for x in rows if headline_kernel(x["Kernel_Name"])]
         if not copy or not kern:
             return None
         scale = (COPY_BYTES / 1024) / max(copy)  # KiB the copy moves / KiB the counter reports
@@ -264,7 +271,10 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a 64 MiB device-to-device copy (the reference kernel for HBM counter scaling)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--kernels", choices=["auto", "dot4", "mfma"], default="auto",
+                    help="kernel family weights are laid out for (librq's RQ_KERNELS)")
     args = ap.parse_args()
+    os.environ["RQ_KERNELS"] = args.kernels  # read by rq_open, here and in the traffic child
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the matvec path has no "
               "multi-GPU code; see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -290,7 +300,7 @@ def main() -> int:
         del src, dst
     T, N, K = 12, 14336, 4096
     r = bench_matvec(torch, gpu, orc, T, N, K, 1, args.steps, args.warmup)
-    log(f"Q4_K {N}x{K} m=1: {r['us']:.2f} us/launch, {r['gbs']:.0f} GB/s "
+    log(f"Q4_K {N}x{K} m=1 ({r['kernels']}): {r['us']:.2f} us/launch, {r['gbs']:.0f} GB/s "
         f"({100 * r['gbs'] / HBM_PEAK_GBS:.1f}% of peak), {r['copies']} copies, check rel {r['check_rel']:.1e}")
 
     if args.all_configs:
@@ -299,7 +309,7 @@ def main() -> int:
                                   ("Q6_K", 14, 128256, 4096, [1]), ("Q4_K", 12, 14336, 4096, [2, 4, 8, 16, 32])]:
             for m in ms:
                 c = bench_matvec(torch, gpu, orc, t, n, k, m, max(256, args.steps // 4), 256)
-                log(f"config {name} {n}x{k} m={m}: {c['us']:.2f} us, {c['gbs']:.0f} GB/s "
+                log(f"config {name} {n}x{k} m={m} ({c['kernels']}): {c['us']:.2f} us, {c['gbs']:.0f} GB/s "
                     f"({100 * c['gbs'] / HBM_PEAK_GBS:.1f}%), copies {c['copies']}")
 
     dec = None
@@ -333,7 +343,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,
-                     "kernel": KERNEL, "kernel_us": round(r["us"], 3), "alg_bytes": r["bytes"]},
+                     "kernel": KERNEL_PREFIX[r["kernels"]] + ("*" if r["kernels"] == "mfma" else ""),
+                     "kernel_us": round(r["us"], 3), "alg_bytes": r["bytes"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

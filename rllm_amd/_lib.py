@@ -21,6 +21,9 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "rq.h")
 
 RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID = 0, 1, 2, 3, 4
 MATVEC_MAX_COLS = 8
+# Kernel families (rq_set_kernels).
+KERNELS_AUTO, KERNELS_DOT4, KERNELS_MFMA = 0, 1, 2
+KERNEL_FAMILIES = {"auto": KERNELS_AUTO, "dot4": KERNELS_DOT4, "mfma": KERNELS_MFMA}
 
 
 class Q8_1Struct(ctypes.Structure):
@@ -57,6 +60,8 @@ _SIGNATURES = {
                               ctypes.POINTER(_i64), _int]),
     "rq_reserve": (_int, [_vp, _i64]),
     "rq_block_dots": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
+    "rq_set_kernels": (_int, [_vp, _int]),
+    "rq_weight_kernels": (_int, [_vp, ctypes.POINTER(_int)]),
 }
 
 _lib: ctypes.CDLL | None = None

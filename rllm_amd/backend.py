@@ -87,6 +87,13 @@ class HipWeight:
         _lib.check(_lib.lib().rq_weight_shape(self.handle, None, None, None, ctypes.byref(n)))
         return n.value
 
+    @property
+    def kernels(self) -> str:
+        """Kernel family the weight is laid out for: "dot4" or "mfma"."""
+        f = ctypes.c_int()
+        _lib.check(_lib.lib().rq_weight_kernels(self.handle, ctypes.byref(f)))
+        return "mfma" if f.value == _lib.KERNELS_MFMA else "dot4"
+
     def free(self) -> None:
         if self.handle:
             h, self.handle = self.handle, None
@@ -165,6 +172,12 @@ class HipBackend:
         """Launch on `stream` from now on (e.g. a graph-capture stream)."""
         _lib.check(_lib.lib().rq_set_stream(self.ctx, stream.cuda_stream))
         self.stream = stream
+
+    def set_kernels(self, family: str) -> None:
+        """Kernel family ("auto", "dot4" or "mfma") for later uploads (rq_set_kernels)."""
+        if family not in _lib.KERNEL_FAMILIES:
+            raise ValueError(f"unknown kernel family {family!r}")
+        _lib.check(_lib.lib().rq_set_kernels(self.ctx, _lib.KERNEL_FAMILIES[family]))
 
     # ---- weights ---------------------------------------------------------------
 

@@ -1,11 +1,13 @@
 """Ahead-of-time build of librq.so for gfx950.
 
-1. hipcc --genco compiles csrc/rq_kernels.hip into one gfx950 code object.
-2. An assembler stub (.incbin) embeds that code object in the library.
+1. hipcc --genco compiles each kernel source (csrc/rq_kernels.hip: the Q8_1
+   pass and the dot4 matvecs; csrc/rq_mmq.hip: the int8-MFMA matvecs) into
+   one gfx950 code object.
+2. An assembler stub (.incbin) embeds the code objects in the library.
 3. g++ compiles the host side (csrc/rq_host.cpp) against the HIP runtime.
 
 The result, rllm_amd/lib/librq.so, is self-contained: rq_open() loads the
-embedded code object with hipModuleLoadData; nothing is compiled at run time.
+embedded code objects with hipModuleLoadData; nothing is compiled at run time.
 
 Usage: python -m rllm_amd.build   (or rllm_amd.build.build()).
 """
@@ -22,6 +24,8 @@ LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "librq.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
+# Kernel sources, one code object each (embedded as <name>_blob).
+KERNEL_SOURCES = ("rq_kernels", "rq_mmq")
 
 # Device code: IEEE-correct f32 division (the Q8_1 scale and codes must match
 # the CPU bit for bit) and no packed-f32 instructions (they have given wrong
@@ -48,21 +52,24 @@ def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    hsaco = os.path.join(BUILD, "rq_kernels.hsaco")
-    _run([hipcc, "--genco", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_kernels.hip"), "-o", hsaco])
     blob = os.path.join(BUILD, "rq_blob.S")
+    stub = []
+    for name in KERNEL_SOURCES:
+        hsaco = os.path.join(BUILD, f"{name}.hsaco")
+        _run([hipcc, "--genco", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, f"{name}.hip"), "-o", hsaco])
+        stub += [
+            "    .section .rodata\n",
+            "    .balign 4096\n",
+            f"    .globl {name}_blob\n",
+            f"    .type {name}_blob, @object\n",
+            f"{name}_blob:\n",
+            f'    .incbin "{hsaco}"\n',
+            "    .byte 0\n",
+            f"    .size {name}_blob, . - {name}_blob\n",
+        ]
+    stub.append('    .section .note.GNU-stack,"",@progbits\n')
     with open(blob, "w") as f:
-        f.write(
-            "    .section .rodata\n"
-            "    .balign 4096\n"
-            "    .globl rq_kernels_blob\n"
-            "    .type rq_kernels_blob, @object\n"
-            "rq_kernels_blob:\n"
-            f'    .incbin "{hsaco}"\n'
-            "    .byte 0\n"
-            "    .size rq_kernels_blob, . - rq_kernels_blob\n"
-            '    .section .note.GNU-stack,"",@progbits\n'
-        )
+        f.write("".join(stub))
     tmp = LIB + ".tmp"
     _run([
         "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -21,7 +22,8 @@
 
 #include "rq_params.h"
 
-extern "C" const unsigned char rq_kernels_blob[];
+extern "C" const unsigned char rq_kernels_blob[];  // rq_kernels.hip: Q8_1 pass, dot4 matvecs
+extern "C" const unsigned char rq_mmq_blob[];      // rq_mmq.hip: int8-MFMA matvecs
 
 namespace {
 
@@ -123,6 +125,16 @@ struct rq_ctx {
     int64_t scap = 0;
     hipFunction_t dots[RQ_NUM_FMTS] = {};
     hipFunction_t repack[RQ_NUM_FMTS] = {};
+    // int8-MFMA kernels (rq_mmq.hip), by format, columns per launch (mp = 1,
+    // 2, 4, 8) and super-blocks per wave (sbw = 2, 4, 8); null where a
+    // format has none.
+    hipModule_t mmq_mod = nullptr;
+    hipFunction_t mmq[RQ_NUM_FMTS][4][3] = {};
+    hipFunction_t mmqf[RQ_NUM_FMTS][3] = {};
+    hipFunction_t mmqd[RQ_NUM_FMTS][4][3] = {};
+    hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
+    int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
+    int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
     hipStream_t stream = nullptr;
 };
 
@@ -133,8 +145,15 @@ struct rq_weight {
     int64_t rows = 0, cols = 0;
     void* base = nullptr;
     size_t bytes = 0;
+    bool mmq = false;  // 16-row tiles for the MFMA kernels; else tiled super-blocks
+    // tiled super-blocks (dot4 kernels)
     RqTiled tiled{};
     size_t main_bytes = 0, tail_bytes = 0;
+    // 16-row tiles (MFMA kernels)
+    const uint8_t* code = nullptr;
+    const uint8_t* hdr = nullptr;
+    int32_t tiles = 0, S2 = 0;
+    size_t code_bytes = 0, hdr_bytes = 0;
 };
 
 namespace {
@@ -256,6 +275,211 @@ rq_status ensure_scratch(rq_ctx* ctx, int64_t values) {
     return RQ_OK;
 }
 
+// ---------------------------------------------------------------------------
+// int8-MFMA kernels over 16-row tiles (rq_mmq.hip, layout in rq_params.h).
+
+constexpr int kMmqMp[4] = {1, 2, 4, 8};
+constexpr int kMmqSbw[3] = {2, 4, 8};
+
+int mmq_mp_index(int mp) { return mp == 1 ? 0 : mp == 2 ? 1 : mp == 4 ? 2 : 3; }
+int mmq_sbw_index(int sbw) { return sbw == 2 ? 0 : sbw == 4 ? 1 : 2; }
+// Most super-blocks per wave the format's kernels exist for (Q8_0 keeps 16 B
+// of codes per window in registers, so it stops at 4).
+int mmq_sbw_max(int fmt) { return fmt == RQ_FMT_Q8_0 ? 4 : 8; }
+int mmq_planes(int fmt) { return fmt == RQ_FMT_Q4_K ? 3 : fmt == RQ_FMT_Q4_0 ? 2 : 1; }
+int mmq_S2(int64_t cols) { return (int)((cols + 511) / 512 * 2); }
+
+// A workgroup holds the ks <= 16 waves of a tile's k-parts.
+bool mmq_supported(int fmt, int64_t cols) {
+    if (fmt == RQ_FMT_Q6_K) return false;
+    const int maxs = mmq_sbw_max(fmt);
+    return (mmq_S2(cols) + maxs - 1) / maxs <= 16;
+}
+
+struct MmqPlan {
+    int mp, sbw, ks, tr;
+    int kxp, z_off, pl_off, part_off, lds;
+};
+
+hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int sbw, bool f32_in, bool dots) {
+    const int si = mmq_sbw_index(sbw), mi = mmq_mp_index(mp);
+    return f32_in ? ctx->mmqf[fmt][si] : dots ? ctx->mmqd[fmt][mi][si] : ctx->mmq[fmt][mi][si];
+}
+
+void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
+    const int NB = 8 * S2;
+    L.kxp = S2 * 256 + 64;  // 64 B of skew: columns start on different LDS banks
+    L.z_off = L.mp * L.kxp;
+    L.pl_off = L.z_off + L.sbw * 256;
+    L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * NB * 4;
+    L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * 4);
+}
+
+// Launch geometry and LDS layout of an rq_mmq launch over weights of S2
+// super-blocks per row and `tiles` tiles in total.
+//   sbw: the fewest super-blocks per wave that keep a tile's k-parts within
+//        one workgroup, raised from 2 to 4 when that still leaves >= 2048
+//        waves (fewer, longer waves stage and reduce less); RQ_MMQ_SBW overrides.
+//   tr:  tiles per workgroup, the smallest that lets every workgroup be
+//        resident at once (per HIP's occupancy for the kernel's registers and
+//        LDS), else the one with the fewest rounds; RQ_MMQ_TR overrides.
+MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int64_t tiles, bool f32_in, bool dots) {
+    MmqPlan L;
+    L.mp = mp;
+    const int maxs = mmq_sbw_max(fmt);
+    int sbw = 2;
+    while (sbw < maxs && (S2 + sbw - 1) / sbw > 16) sbw *= 2;
+    if (ctx->mmq_sbw >= sbw && ctx->mmq_sbw <= maxs && (ctx->mmq_sbw & (ctx->mmq_sbw - 1)) == 0)
+        sbw = ctx->mmq_sbw;
+    else if (sbw == 2 && tiles * ((S2 + 3) / 4) >= 2048)
+        sbw = 4;
+    L.sbw = sbw;
+    L.ks = (S2 + sbw - 1) / sbw;
+    if (ctx->mmq_tr > 0) {
+        L.tr = std::max(1, std::min(ctx->mmq_tr, 16 / L.ks));
+        mmq_layout(fmt, S2, dots, L);
+        return L;
+    }
+    hipFunction_t f = mmq_kernel(ctx, fmt, mp, sbw, f32_in, dots);
+    int64_t best_rounds = -1;
+    MmqPlan best = L;
+    for (int tr = 1; tr * L.ks <= 16; tr *= 2) {
+        MmqPlan c = L;
+        c.tr = tr;
+        mmq_layout(fmt, S2, dots, c);
+        if (c.lds > ctx->lds_wide) continue;
+        int per_cu = 0;
+        if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * L.ks * tr, (size_t)c.lds) !=
+                      hipSuccess || per_cu < 1)
+            per_cu = 1;
+        const int64_t wgs = (tiles + tr - 1) / tr, slots = (int64_t)per_cu * ctx->cus;
+        const int64_t rounds = (wgs + slots - 1) / slots;
+        if (best_rounds < 0 || rounds < best_rounds) {
+            best_rounds = rounds;
+            best = c;
+        }
+        if (rounds <= 1) break;
+    }
+    if (best_rounds < 0) {  // nothing fits: report the smallest layout's size
+        best.tr = 1;
+        mmq_layout(fmt, S2, dots, best);
+    }
+    return best;
+}
+
+int pow2_at_least(int v) {
+    int p = 1;
+    while (p < v) p *= 2;
+    return p;
+}
+
+// MFMA matvec / block-dot launches over `count` same-type weights of width k.
+// The m columns run in the fewest near-equal groups of <= 8 whose staging fits
+// the LDS a workgroup may use; every launch reads the weights once. xf set:
+// one f32 column quantized while staging (rq_mmqf_*); dots set: int32 block
+// dots instead of the f32 sums (rq_mmqd_*; `outs` are then int32 arrays).
+rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
+                     const rq_weight* const* ws, void* const* outs, int count, bool dots) {
+    const int fmt = ws[0]->fmt;
+    const int64_t k = ws[0]->cols, U = k / 32;
+    const int S2 = ws[0]->S2;
+    int64_t tiles = 0;
+    for (int i = 0; i < count; i++) tiles += ws[i]->tiles;
+    int64_t ngroups = (m + 7) / 8;
+    MmqPlan L;
+    for (;;) {
+        const int nc = (int)((m + ngroups - 1) / ngroups);
+        L = mmq_plan(ctx, fmt, S2, xf ? 1 : pow2_at_least(nc), tiles, xf != nullptr, dots);
+        if (L.lds <= ctx->lds_wide) break;
+        if (nc == 1)
+            return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage (%d bytes of LDS)", (long long)k, L.lds);
+        ngroups = (m + nc / 2 - 1) / (nc / 2);
+    }
+    for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
+        const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
+        const MmqPlan P = mmq_plan(ctx, fmt, S2, xf ? 1 : pow2_at_least(nc), tiles, xf != nullptr, dots);
+        RqMmqParams p;
+        memset(&p, 0, sizeof p);
+        int64_t wgs = 0;
+        for (int i = 0; i < count; i++) {
+            const rq_weight* w = ws[i];
+            p.t[i].code = w->code;
+            p.t[i].hdr = w->hdr;
+            p.t[i].out = dots ? (void*)((int32_t*)outs[i] + g0 * w->rows * U) : (void*)((float*)outs[i] + g0 * w->rows);
+            p.t[i].n = (int32_t)w->rows;
+            p.t[i].tiles = w->tiles;
+            p.t[i].wg_start = (int32_t)wgs;
+            wgs += (w->tiles + P.tr - 1) / P.tr;
+        }
+        if (xf) {
+            p.xf = xf + g0 * k;
+        } else {
+            p.xq = xq + g0 * k;
+            p.xd = xd + g0 * U;
+        }
+        p.count = count;
+        p.m = nc;
+        p.k = (int32_t)k;
+        p.S2 = S2;
+        p.ks = P.ks;
+        p.tr = P.tr;
+        p.kxp = P.kxp;
+        p.z_off = P.z_off;
+        p.pl_off = P.pl_off;
+        p.part_off = P.part_off;
+        hipFunction_t f = mmq_kernel(ctx, fmt, P.mp, P.sbw, xf != nullptr, dots);
+        if (!f) return fail(RQ_ERR_UNSUPPORTED, "matvec: no MFMA kernel for %d columns, %d super-blocks per wave", P.mp, P.sbw);
+        rq_status st = launch(ctx, f, dots ? "rq_mmqd" : xf ? "rq_mmqf" : "rq_mmq", (uint64_t)wgs, &p, (unsigned)P.lds,
+                              (unsigned)(64 * P.ks * P.tr));
+        if (st != RQ_OK) return st;
+        g0 += nc;
+    }
+    return RQ_OK;
+}
+
+// 16-row tiles back to GGUF rows (host side of rq_weight_to_gguf).
+void mmq_to_gguf(const rq_weight* w, const uint8_t* code, const uint8_t* hdr, uint8_t* out) {
+    const int fmt = w->fmt, S2 = w->S2;
+    const int64_t k = w->cols, U = k / 32, rb = rq_row_bytes(w->type, k);
+    const bool nib = fmt != RQ_FMT_Q8_0;
+    auto code_of = [&](int64_t r, int64_t e) -> int {
+        const int64_t T = r / 16, n = r % 16, win = e / 64, g = (e % 64) / 16, b = e % 16;
+        if (nib) {
+            const uint8_t v = code[((T * 2 * S2 + win / 2) * 64 + 16 * g + n) * 16 + b];
+            return (win & 1) ? ((v >> 4) ^ 8) : (v & 0xF);
+        }
+        return (int)(int8_t)code[((T * 4 * S2 + win) * 64 + 16 * g + n) * 16 + b];
+    };
+    auto hdr_of = [&](int64_t r, int64_t s) { return hdr + (((r / 16) * S2 + s) * 16 + r % 16) * 16; };
+    for (int64_t r = 0; r < w->rows; r++) {
+        uint8_t* row = out + r * rb;
+        memset(row, 0, (size_t)rb);
+        if (fmt == RQ_FMT_Q4_K) {
+            for (int64_t s = 0; s < k / 256; s++) {
+                uint8_t* b = row + s * 144;
+                memcpy(b, hdr_of(r, s), 16);
+                for (int i = 0; i < 256; i++) {
+                    const int q = code_of(r, 256 * s + i), c = i / 64, rr = i % 64;
+                    b[16 + 32 * c + rr % 32] |= (uint8_t)(rr < 32 ? q : q << 4);
+                }
+            }
+        } else {
+            const int bb = fmt == RQ_FMT_Q4_0 ? 18 : 34;
+            for (int64_t bi = 0; bi < U; bi++) {
+                uint8_t* b = row + bi * bb;
+                memcpy(b, hdr_of(r, bi / 8) + 2 * (bi % 8), 2);
+                for (int i = 0; i < 32; i++) {
+                    const int q = code_of(r, 32 * bi + i);
+                    if (fmt == RQ_FMT_Q4_0)
+                        b[2 + i % 16] |= (uint8_t)(i < 16 ? q : q << 4);
+                    else
+                        b[2 + i] = (uint8_t)q;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -279,6 +503,7 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     ctx->device = device;
     auto bail = [&](rq_status st) {
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
+        if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
         delete ctx;
         return st;
     };
@@ -291,6 +516,13 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     if (strncmp(ctx->arch, "gfx950", 6) != 0)
         return bail(fail(RQ_ERR_UNSUPPORTED, "rq_open: device %d is %s; librq is built for gfx950 only", device, ctx->arch));
     if ((e = hipModuleLoadData(&ctx->mod, rq_kernels_blob)) != hipSuccess) return bail(hip_fail("hipModuleLoadData", e));
+    if ((e = hipModuleLoadData(&ctx->mmq_mod, rq_mmq_blob)) != hipSuccess) return bail(hip_fail("hipModuleLoadData", e));
+    auto getm = [&](hipModule_t mod, hipFunction_t* f, const char* name) -> rq_status {
+        hipError_t ge = hipModuleGetFunction(f, mod, name);
+        if (ge != hipSuccess)
+            return fail(RQ_ERR_BACKEND, "hipModuleGetFunction(%s): %s (%d)", name, hipGetErrorName(ge), (int)ge);
+        return RQ_OK;
+    };
     auto get = [&](hipFunction_t* f, const char* name) -> rq_status {
         hipError_t ge = hipModuleGetFunction(f, ctx->mod, name);
         if (ge != hipSuccess)
@@ -316,8 +548,41 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
         snprintf(name, sizeof name, "rq_repack_%s", kFmtSuffix[f]);
         st = get(&ctx->repack[f], name);
     }
+    for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
+        if (f == RQ_FMT_Q6_K) continue;
+        snprintf(name, sizeof name, "rq_mmq_repack_%s", kFmtSuffix[f]);
+        if ((st = getm(ctx->mmq_mod, &ctx->mmq_repack[f], name)) != RQ_OK) break;
+        for (int si = 0; si < 3 && st == RQ_OK; si++) {
+            if (kMmqSbw[si] > mmq_sbw_max(f)) continue;
+            snprintf(name, sizeof name, "rq_mmqf_%s_%d", kFmtSuffix[f], kMmqSbw[si]);
+            st = getm(ctx->mmq_mod, &ctx->mmqf[f][si], name);
+            for (int mi = 0; mi < 4 && st == RQ_OK; mi++) {
+                snprintf(name, sizeof name, "rq_mmq_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
+                if ((st = getm(ctx->mmq_mod, &ctx->mmq[f][mi][si], name)) != RQ_OK) break;
+                snprintf(name, sizeof name, "rq_mmqd_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
+                st = getm(ctx->mmq_mod, &ctx->mmqd[f][mi][si], name);
+            }
+        }
+    }
     if (st != RQ_OK) return bail(st);
+    // Defaults and tuning overrides from the environment.
+    if (const char* v = getenv("RQ_KERNELS")) {
+        if (!strcmp(v, "dot4")) ctx->kernels = RQ_KERNELS_DOT4;
+        else if (!strcmp(v, "mfma")) ctx->kernels = RQ_KERNELS_MFMA;
+        else if (!strcmp(v, "auto") || !*v) ctx->kernels = RQ_KERNELS_AUTO;
+        else return bail(fail(RQ_ERR_INVALID, "rq_open: RQ_KERNELS=%s (auto, dot4 or mfma)", v));
+    }
+    if (const char* v = getenv("RQ_MMQ_SBW")) ctx->mmq_sbw = atoi(v);
+    if (const char* v = getenv("RQ_MMQ_TR")) ctx->mmq_tr = std::max(0, std::min(16, atoi(v)));
     *out = ctx;
+    return RQ_OK;
+}
+
+extern "C" rq_status rq_set_kernels(rq_ctx* ctx, int family) {
+    if (!ctx) return fail(RQ_ERR_INVALID, "rq_set_kernels: null context");
+    if (family != RQ_KERNELS_AUTO && family != RQ_KERNELS_DOT4 && family != RQ_KERNELS_MFMA)
+        return fail(RQ_ERR_INVALID, "rq_set_kernels: unknown family %d", family);
+    ctx->kernels = family;
     return RQ_OK;
 }
 
@@ -330,6 +595,7 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         if (ctx->sd) (void)hipFree(ctx->sd);
         if (ctx->ss) (void)hipFree(ctx->ss);
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
+        if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
     }
     delete ctx;
     return st;
@@ -374,21 +640,37 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
     w->fmt = fmt;
     w->rows = rows;
     w->cols = cols;
-    tile_geometry(rows, cols, w->tiled);
-    const int64_t slots = (int64_t)w->tiled.T * w->tiled.R * w->tiled.S;
-    w->main_bytes = (size_t)(slots * rq_chunks(fmt) * 16);
-    w->tail_bytes = fmt == RQ_FMT_Q6_K ? (size_t)(slots * 2) : 0;
-    const size_t tail_off = align_up(w->main_bytes, kPlaneAlign);
-    const size_t total = align_up(tail_off + w->tail_bytes, kPlaneAlign);
+    // AUTO lays weights out for the dot4 kernels, the faster family at one
+    // activation column (decode); MFMA is chosen explicitly (continuous batching).
+    w->mmq = ctx->kernels == RQ_KERNELS_MFMA && mmq_supported(fmt, cols);
+    size_t total = 0;
+    if (w->mmq) {
+        w->S2 = mmq_S2(cols);
+        w->tiles = (int32_t)((rows + 15) / 16);
+        w->code_bytes = (size_t)w->tiles * 16 * w->S2 * (fmt == RQ_FMT_Q8_0 ? 256 : 128);
+        w->hdr_bytes = (size_t)w->tiles * w->S2 * 256;
+        total = align_up(align_up(w->code_bytes, kPlaneAlign) + w->hdr_bytes, kPlaneAlign);
+    } else {
+        tile_geometry(rows, cols, w->tiled);
+        const int64_t slots = (int64_t)w->tiled.T * w->tiled.R * w->tiled.S;
+        w->main_bytes = (size_t)(slots * rq_chunks(fmt) * 16);
+        w->tail_bytes = fmt == RQ_FMT_Q6_K ? (size_t)(slots * 2) : 0;
+        total = align_up(align_up(w->main_bytes, kPlaneAlign) + w->tail_bytes, kPlaneAlign);
+    }
     hipError_t e = hipMalloc(&w->base, total);
     if (e != hipSuccess) {
         delete w;
         return hip_fail("hipMalloc", e);
     }
     w->bytes = total;
-    w->tiled.main = (const uint8_t*)w->base;
-    w->tiled.tail = (const uint8_t*)w->base + tail_off;
-    // Padding slots (rows past the end, blocks past a partial super-block) stay zero.
+    if (w->mmq) {
+        w->code = (const uint8_t*)w->base;
+        w->hdr = (const uint8_t*)w->base + align_up(w->code_bytes, kPlaneAlign);
+    } else {
+        w->tiled.main = (const uint8_t*)w->base;
+        w->tiled.tail = (const uint8_t*)w->base + align_up(w->main_bytes, kPlaneAlign);
+    }
+    // Padding (rows past the end, blocks past k) stays zero.
     e = hipMemsetAsync(w->base, 0, total, ctx->stream);
 
     const int64_t chunk_rows = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)(kUploadChunkBytes / rb)));
@@ -407,17 +689,31 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
             st = hip_fail("hipMemcpyAsync", e);
             break;
         }
-        RqRepackParams p;
-        memset(&p, 0, sizeof p);
-        p.raw = (const uint8_t*)staging;
-        p.main = (uint8_t*)w->tiled.main;
-        p.tail = (uint8_t*)w->tiled.tail;
-        p.row0 = row0;
-        p.rows = n;
-        p.S = w->tiled.S;
-        p.R = w->tiled.R;
-        p.k = (int32_t)cols;
-        st = launch(ctx, ctx->repack[fmt], "rq_repack", (uint64_t)((n * p.S + RQ_THREADS - 1) / RQ_THREADS), &p);
+        if (w->mmq) {
+            RqMmqRepackParams p;
+            memset(&p, 0, sizeof p);
+            p.raw = (const uint8_t*)staging;
+            p.code = (uint8_t*)w->code;
+            p.hdr = (uint8_t*)w->hdr;
+            p.row0 = row0;
+            p.rows = n;
+            p.S2 = w->S2;
+            p.k = (int32_t)cols;
+            st = launch(ctx, ctx->mmq_repack[fmt], "rq_mmq_repack",
+                        (uint64_t)((n * p.S2 + RQ_THREADS - 1) / RQ_THREADS), &p);
+        } else {
+            RqRepackParams p;
+            memset(&p, 0, sizeof p);
+            p.raw = (const uint8_t*)staging;
+            p.main = (uint8_t*)w->tiled.main;
+            p.tail = (uint8_t*)w->tiled.tail;
+            p.row0 = row0;
+            p.rows = n;
+            p.S = w->tiled.S;
+            p.R = w->tiled.R;
+            p.k = (int32_t)cols;
+            st = launch(ctx, ctx->repack[fmt], "rq_repack", (uint64_t)((n * p.S + RQ_THREADS - 1) / RQ_THREADS), &p);
+        }
     }
     // Keep `staging` alive until the repack kernels have read it.
     e = hipStreamSynchronize(ctx->stream);
@@ -452,6 +748,12 @@ extern "C" rq_status rq_weight_shape(const rq_weight* w, int* type, int64_t* row
     return RQ_OK;
 }
 
+extern "C" rq_status rq_weight_kernels(const rq_weight* w, int* family) {
+    if (!w || !family) return fail(RQ_ERR_INVALID, "rq_weight_kernels: null argument");
+    *family = w->mmq ? RQ_KERNELS_MFMA : RQ_KERNELS_DOT4;
+    return RQ_OK;
+}
+
 extern "C" rq_status rq_weight_to_gguf(rq_ctx* ctx, const rq_weight* w, void* gguf, size_t len) {
     if (!ctx || !w || !gguf) return fail(RQ_ERR_INVALID, "rq_weight_to_gguf: null argument");
     const int64_t rb = rq_row_bytes(w->type, w->cols);
@@ -459,6 +761,13 @@ extern "C" rq_status rq_weight_to_gguf(rq_ctx* ctx, const rq_weight* w, void* gg
     rq_status st = bind(ctx);
     if (st != RQ_OK) return st;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (w->mmq) {
+        std::vector<uint8_t> codep(w->code_bytes), hdrp(w->hdr_bytes);
+        HIP_TRY(hipMemcpy(codep.data(), w->code, w->code_bytes, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hdrp.data(), w->hdr, w->hdr_bytes, hipMemcpyDeviceToHost));
+        mmq_to_gguf(w, codep.data(), hdrp.data(), (uint8_t*)gguf);
+        return RQ_OK;
+    }
     std::vector<uint8_t> mainp(w->main_bytes), tailp(w->tail_bytes);
     HIP_TRY(hipMemcpy(mainp.data(), w->tiled.main, w->main_bytes, hipMemcpyDeviceToHost));
     if (w->tail_bytes) HIP_TRY(hipMemcpy(tailp.data(), w->tiled.tail, w->tail_bytes, hipMemcpyDeviceToHost));
@@ -549,6 +858,8 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if (ws[i]->type != ws[0]->type)
             return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
                         type_name(ws[i]->type));
+        if (ws[i]->mmq != ws[0]->mmq)
+            return fail(RQ_ERR_SHAPE, "matvec: weights laid out for different kernel families in one launch");
         if (ws[i]->cols != ws[0]->cols)
             return fail(RQ_ERR_SHAPE, "matmul_many: mixed input widths %lld and %lld", (long long)ws[0]->cols,
                         (long long)ws[i]->cols);
@@ -560,6 +871,7 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if ((st = check_len("matmul out", out_lens[i], m * ws[i]->rows)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
+    if (ws[0]->mmq) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
     return matvec_launch(ctx, xq->qs, xq->d, nullptr, m, ws, outs, count);
 }
 
@@ -612,13 +924,18 @@ extern "C" rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, 
                          (uint64_t)((qp.nblocks * 8 + RQ_THREADS - 1) / RQ_THREADS), &qp)) != RQ_OK)
             return st;
     }
-    // One launch per run of <= 3 same-type weights.
+    // One launch per run of <= 3 weights of one type and kernel family.
     int i = 0;
     while (i < count) {
         int g = 1;
-        while (g < RQ_MV_TARGETS && i + g < count && ws[i + g]->type == ws[i]->type) g++;
-        st = fused ? matvec_launch(ctx, nullptr, nullptr, x, m, ws + i, outs + i, g)
-                   : matvec_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, outs + i, g);
+        while (g < RQ_MV_TARGETS && i + g < count && ws[i + g]->type == ws[i]->type && ws[i + g]->mmq == ws[i]->mmq)
+            g++;
+        if (ws[i]->mmq)
+            st = fused ? mmq_launch(ctx, nullptr, nullptr, x, m, ws + i, (void* const*)(outs + i), g, false)
+                       : mmq_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, (void* const*)(outs + i), g, false);
+        else
+            st = fused ? matvec_launch(ctx, nullptr, nullptr, x, m, ws + i, outs + i, g)
+                       : matvec_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, outs + i, g);
         if (st != RQ_OK) return st;
         i += g;
     }
@@ -641,6 +958,10 @@ extern "C" rq_status rq_block_dots(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, co
     if ((st = check_len("block_dots out", dots_len, m * w->rows * nb)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
+    if (w->mmq) {
+        void* out = dots;
+        return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, &w, &out, 1, true);
+    }
     RqDotsParams p;
     memset(&p, 0, sizeof p);
     p.w = w->tiled;

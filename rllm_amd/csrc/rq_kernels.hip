@@ -17,43 +17,11 @@
 // across the wave. A row's partial sums meet in a DPP reduction within its
 // lane group.
 
-#include <hip/hip_runtime.h>
-
 #include "rq_params.h"
-
-typedef uint8_t u8;
-typedef uint16_t u16;
-typedef uint32_t u32;
-typedef uint64_t u64;
+#include "rq_device.h"
 
 // ---------------------------------------------------------------------------
-// Small helpers
-
-__device__ __forceinline__ float h2f(u32 h) { return (float)__builtin_bit_cast(_Float16, (u16)h); }
-
-// f32 -> f16 with v_cvt_f16_f32 (round to nearest even).
-__device__ __forceinline__ u16 f2h(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
-
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
-}
-
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, dpp_i<CTRL, ROW_MASK>(__builtin_bit_cast(int, v)));
-}
-
-// DPP controls (gfx9 encoding).
-#define DPP_QUAD_1032 0xB1  // quad_perm [1,0,3,2]
-#define DPP_QUAD_2301 0x4E  // quad_perm [2,3,0,1]
-#define DPP_ROW_MIRROR 0x140
-#define DPP_ROW_HALF_MIRROR 0x141
-#define DPP_ROW_BCAST15 0x142
-
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
+// Lane-group reductions
 
 // Sums over aligned lane groups of `g` lanes (g = 1, 2, 4, 8, 16, 32 or 64;
 // wave-uniform), every lane of the wave active. Afterwards each lane holds
@@ -75,58 +43,12 @@ __device__ __forceinline__ bool group_leader(int lane, int g) {
     return g == 32 ? (lane & 31) == 16 : (g == 64 ? lane == 0 : (lane & (g - 1)) == 0);
 }
 
-// v_dot4_i32_i8: c + sum of the four signed byte products.
-__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-// Streaming 16-byte load: weights are read once, so the nontemporal hint
-// keeps them from displacing reusable lines (activations) in the caches.
-__device__ __forceinline__ int4 ld16_nt(const u8* p) {
-    typedef int v4i __attribute__((ext_vector_type(4)));
-    const v4i v = __builtin_nontemporal_load((const v4i*)p);
-    return make_int4(v.x, v.y, v.z, v.w);
-}
-
 // ---------------------------------------------------------------------------
 // Q8_1 activations. Eight lanes per 32-value block, four values each (one
 // float4 load and one packed dword store per lane). amax and the code sum
 // meet across the eight lanes with DPP; every lane of an 8-lane group is
 // active (the grid is a whole number of groups and groups exit together).
-//
-// Numerics (bit-exact with the CPU restatement): d = amax / 127 and x / d
-// are IEEE divisions (built with -fhip-fp32-correctly-rounded-divide-sqrt),
-// rintf rounds half to even, f16 conversion rounds to nearest even.
-
-// Codes q_i = rint(x_i / d) of n values of one block, d = amax / 127 with
-// amax >= |x_i|: the IEEE quotient rounded half to even, without dividing
-// per value where that is provably unnecessary.
-//
-// Fast path: r = 1 / d (IEEE) and t = x * r. Each rounding is a relative
-// error of at most 2^-24, and |x / d| <= 190.5 (127 (1 + 2^-23) unless d is
-// subnormal, where d = RN(amax / 127) can undershoot by up to a third), so
-// |t - x / d| <= 190.5 * (2^-23 + 2^-48) < 2.3e-5 (t is subnormal only when
-// x / d is far below 1/2, where both round to 0). When t lies farther than
-// 2^-14 (6.1e-5) from every half-integer, x / d falls strictly inside the same
-// rounding interval and rint(x / d) = rint(t). A lane any of whose values
-// misses that window recomputes all of them with the division; so do d = 0
-// (r infinite, t NaN) and infinite or NaN inputs, where the window test is
-// false. The codes are therefore the division's in every case.
-template <int N>
-__device__ __forceinline__ void q8_codes(const float* x, float d, int* q) {
-#pragma clang fp contract(off)
-    const float r = 1.0f / d;
-    bool near_tie = false;
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        const float t = x[i] * r;
-        const float rt = rintf(t);
-        near_tie |= !(fabsf(t - rt) < 0.49993896484375f);  // 0.5 - 2^-14
-        q[i] = (int)rt;
-    }
-    if (near_tie) {
-#pragma unroll
-        for (int i = 0; i < N; i++) q[i] = d > 0.f ? (int)rintf(x[i] / d) : 0;
-    }
-}
+// Rounding: q8_codes (rq_device.h).
 
 extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_quantize_q8_1(RqQuantParams p) {
     const int64_t t = (int64_t)blockIdx.x * RQ_THREADS + threadIdx.x;
@@ -550,7 +472,9 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     int ti = 0;
     if (P.count > 1 && gwave >= P.t[1].wave_start) ti = 1;
     if (P.count > 2 && gwave >= P.t[2].wave_start) ti = 2;
-    const RqMvTarget& T = P.t[ti];
+    // By value, selected from fields at static kernarg offsets (a reference
+    // indexed by ti reloads its fields with dependent scalar loads at each use).
+    const RqMvTarget T = ti == 0 ? P.t[0] : (ti == 1 ? P.t[1] : P.t[2]);
     const int t = gwave - T.wave_start;  // this wave's tile
     const bool has_tile = t < T.w.T;     // wave-uniform
     const int R = T.w.R, slots = R * S;

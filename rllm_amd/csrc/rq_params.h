@@ -109,3 +109,72 @@ struct RqDotsParams {
     int32_t m;
     int32_t pad;
 };
+
+// ---------------------------------------------------------------------------
+// MFMA weight layout ("16-row tiles", the rq_mmq_* kernels of rq_mmq.hip).
+//
+// Rows are grouped in tiles of 16 (tile T holds rows 16T .. 16T + 15; rows past
+// n are zero). S2 = ceil(k / 512) * 2 super-blocks of 256 elements per row
+// (super-blocks and blocks past k are zero). A window is 64 consecutive
+// elements of a row; within a window, k-group g = 0..3 is elements 16g ..
+// 16g + 15. Lane l = 16g + n of a wave serves row n, k-group g, which is how
+// the B operand of v_mfma_i32_16x16x64_i8 is laid out.
+//
+// Code plane, 1 KB per block, lane l's 16 bytes at block * 1024 + l * 16:
+//   Q4_K, Q4_0  block (T, p) = T * 2 * S2 + p for window pair p (128
+//               elements): byte b of lane (n, g) holds in its low nibble the
+//               code of element 128p + 16g + b (window 2p) and in its high
+//               nibble the code of element 128p + 64 + 16g + b (window 2p + 1)
+//               XOR 8, so that masking the byte with 0xF0 gives the signed
+//               value 16 * (code - 8).
+//   Q8_0        block (T, w) = T * 4 * S2 + w for window w: byte b of lane
+//               (n, g) is the int8 code of element 64w + 16g + b.
+// Header plane, 256 B per (tile, super-block s): row n's 16 bytes at
+//   ((T * S2 + s) * 16 + n) * 16:
+//   Q4_K        GGUF bytes 0..15 of the super-block (f16 d, f16 dmin, the 12
+//               bytes of packed 6-bit scales and mins), verbatim;
+//   Q4_0, Q8_0  the f16 scales d of the super-block's eight 32-element blocks.
+// Bytes per row and super-block equal GGUF's (144 / 144 / 272): the repack
+// moves bits and rounds nothing.
+
+// Super-blocks per wave of an rq_mmq launch (RqMmqParams.ks waves per tile).
+#define RQ_MMQ_SBW_MAX 4
+
+struct RqMmqTarget {
+    const uint8_t* code;  // code plane
+    const uint8_t* hdr;   // header plane
+    void* out;            // f32 out[a * n + r] (dots kernel: int32 dots)
+    int32_t n;            // rows
+    int32_t tiles;        // ceil(n / 16)
+    int32_t wg_start;     // first workgroup of this target
+    int32_t pad;
+};
+
+struct RqMmqParams {
+    RqMmqTarget t[RQ_MV_TARGETS];
+    const int8_t* xq;    // Q8_1 codes, column a at xq + a * k
+    const uint16_t* xd;  // Q8_1 f16 scales, column a at xd + a * k / 32
+    const float* xf;     // f32 activations (rq_mmqf_*), column a at xf + a * k
+    int32_t count;       // targets
+    int32_t m;           // activation columns of this launch (<= the kernel's MP)
+    int32_t k;           // columns
+    int32_t S2;          // super-blocks per row (even)
+    int32_t ks;          // waves (k-parts) per tile
+    int32_t tr;          // tiles per workgroup
+    // Workgroup LDS (byte offsets, set by the host): staged activation codes
+    // (column a at a * kxp), a zero region of sbw * 256 bytes at z_off, the
+    // per-block activation planes at pl_off, the waves' partial sums at part_off.
+    int32_t kxp;
+    int32_t z_off;
+    int32_t pl_off;
+    int32_t part_off;
+};
+
+struct RqMmqRepackParams {
+    const uint8_t* raw;  // GGUF bytes of rows [row0, row0 + rows)
+    uint8_t* code;
+    uint8_t* hdr;
+    int64_t row0;
+    int64_t rows;
+    int32_t S2, k, pad[2];
+};

@@ -35,3 +35,13 @@ def gpu():
     yield b
     b.synchronize()
     b.close()
+
+
+@pytest.fixture(params=["dot4", "mfma"])
+def gpuk(gpu, request):
+    """`gpu` with later uploads laid out for one kernel family (rq_set_kernels);
+    tests taking it run once per family."""
+    gpu.set_kernels(request.param)
+    gpu.kernel_family = request.param
+    yield gpu
+    gpu.set_kernels("auto")

@@ -30,35 +30,35 @@ def _capture(gpu, fn):
     return g
 
 
-def test_matmul_graph_replays(gpu, orc):
+def test_matmul_graph_replays(gpuk, orc):
     """Backend::matmul_many at m = 1 (quantize while staging) and m = 3 (the
     reserved Q8_1 scratch) inside one graph."""
     k = 14336
     spec = [(14, 96), (12, 40), (8, 33)]
-    wgs = [upload(gpu, t, make_weight(orc, t, n, k, 70 + i, "normal"), n, k) for i, (t, n) in enumerate(spec)]
-    gpu.reserve(3 * k)
-    x1 = gpu.from_host(orc.normal(1, k))
-    x3 = gpu.from_host(orc.normal(2, 3 * k))
-    g_out1 = [gpu.alloc(n) for _, n in spec]
-    g_out3 = [gpu.alloc(3 * n) for _, n in spec]
+    wgs = [upload(gpuk, t, make_weight(orc, t, n, k, 70 + i, "normal"), n, k) for i, (t, n) in enumerate(spec)]
+    gpuk.reserve(3 * k)
+    x1 = gpuk.from_host(orc.normal(1, k))
+    x3 = gpuk.from_host(orc.normal(2, 3 * k))
+    g_out1 = [gpuk.alloc(n) for _, n in spec]
+    g_out3 = [gpuk.alloc(3 * n) for _, n in spec]
 
     def step():
-        gpu.matmul_many(x1, wgs, g_out1, 1)
-        gpu.matmul_many(x3, wgs, g_out3, 3)
+        gpuk.matmul_many(x1, wgs, g_out1, 1)
+        gpuk.matmul_many(x3, wgs, g_out3, 3)
 
-    g = _capture(gpu, step)
+    g = _capture(gpuk, step)
     for rep in range(4):
-        x1.copy_(torch.from_numpy(orc.normal(10 + rep, k)).to(gpu.device))
-        x3.copy_(torch.from_numpy(orc.normal(20 + rep, 3 * k)).to(gpu.device))
+        x1.copy_(torch.from_numpy(orc.normal(10 + rep, k)).to(gpuk.device))
+        x3.copy_(torch.from_numpy(orc.normal(20 + rep, 3 * k)).to(gpuk.device))
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         got1 = [o.clone() for o in g_out1]
         got3 = [o.clone() for o in g_out3]
-        e_out1 = [gpu.alloc(n) for _, n in spec]
-        e_out3 = [gpu.alloc(3 * n) for _, n in spec]
-        gpu.matmul_many(x1, wgs, e_out1, 1)
-        gpu.matmul_many(x3, wgs, e_out3, 3)
+        e_out1 = [gpuk.alloc(n) for _, n in spec]
+        e_out3 = [gpuk.alloc(3 * n) for _, n in spec]
+        gpuk.matmul_many(x1, wgs, e_out1, 1)
+        gpuk.matmul_many(x3, wgs, e_out3, 3)
         torch.cuda.synchronize()
         for a, b in zip(got1 + got3, e_out1 + e_out3):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"replay {rep} differs from eager"

@@ -1,0 +1,140 @@
+"""GPU parity of the int8-MFMA kernels (rq_mmq.hip) through the C-ABI.
+
+The MFMA kernels split the activation columns into classes of 1, 2, 4 or 8
+per launch, stage k in super-block parts of 2, 4 or 8 per wave, pad k to
+an even number of 256-element super-blocks and rows to tiles of 16; these
+tests walk those cases against the CPU oracle (block dots bit-exact, f32
+outputs within 1e-3 of the integer path's exact value) and against the dot4
+kernels on identical inputs.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import make_weight, q8_1_to_device, upload
+
+pytestmark = pytest.mark.gpu
+
+TOL_B = 1e-3
+MMQ_TYPES = {"Q4_0": 2, "Q8_0": 8, "Q4_K": 12}
+
+
+@pytest.fixture
+def mfma(gpu):
+    gpu.set_kernels("mfma")
+    yield gpu
+    gpu.set_kernels("auto")
+
+
+def _run(gpu, orc, t, n, k, m, seed, kind="random", dots=True):
+    w = make_weight(orc, t, n, k, seed, kind)
+    wg = upload(gpu, t, w, n, k)
+    assert wg.kernels == "mfma"
+    x = orc.normal(seed + 1, m * k, 0.0, 1.0)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    xq = q8_1_to_device(gpu, qs, d, s)
+    out = gpu.alloc(m * n)
+    gpu.matvec(xq, wg, out, m)
+    orc.assert_close(f"type {t} {n}x{k} m={m}", orc.matvec_q8_1(t, w, n, k, qs, d, m), gpu.to_host(out, m * n), TOL_B)
+    if dots:
+        got = gpu.block_dots(xq, wg, m).cpu().numpy()
+        want = orc.block_dots(t, w, n, k, qs, m)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"{bad.size} block dots differ, first {bad[0]}: {got[bad[0]]} vs {want[bad[0]]}"
+
+
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 32, 33])
+def test_mmq_column_classes(mfma, orc, tname, m):
+    """Every column class (1, 2, 4, 8 per launch), padded classes and several launches."""
+    _run(mfma, orc, MMQ_TYPES[tname], 45, 1024, m, 300 + m)
+
+
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
+@pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480])
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_mmq_widths(mfma, orc, tname, k, m):
+    """Odd super-block counts (zero padding to an even count), 2/4/8 super-blocks per wave."""
+    t = MMQ_TYPES[tname]
+    if t == 8 and k > 16384:
+        pytest.skip("Q8_0 over 16384 columns runs the dot4 kernels")
+    _run(mfma, orc, t, 33, k, m, 17 * k + m, kind="normal")
+
+
+@pytest.mark.parametrize("tname", ["Q4_0", "Q8_0"])
+@pytest.mark.parametrize("k", [32, 32 * 65, 32 * 17])
+def test_mmq_partial_super_blocks(mfma, orc, tname, k):
+    """Widths that are not a multiple of 256: missing blocks are zeros."""
+    _run(mfma, orc, MMQ_TYPES[tname], 21, k, 2, 11 + k)
+
+
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
+@pytest.mark.parametrize("m", [1, 4])
+def test_mmq_matches_dot4(gpu, orc, tname, m):
+    """The same weight in both layouts: identical int32 block dots, f32 sums
+    that differ only by accumulation order."""
+    t, n, k = MMQ_TYPES[tname], 200, 4096
+    w = make_weight(orc, t, n, k, 55 + m, "normal")
+    gpu.set_kernels("dot4")
+    w4 = upload(gpu, t, w, n, k)
+    gpu.set_kernels("mfma")
+    wm = upload(gpu, t, w, n, k)
+    gpu.set_kernels("auto")
+    assert (w4.kernels, wm.kernels) == ("dot4", "mfma")
+    x = orc.normal(77 + m, m * k, 0.0, 1.0)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    xq = q8_1_to_device(gpu, qs, d, s)
+    assert np.array_equal(gpu.block_dots(xq, w4, m).cpu().numpy(), gpu.block_dots(xq, wm, m).cpu().numpy())
+    o4, om = gpu.alloc(m * n), gpu.alloc(m * n)
+    gpu.matvec(xq, w4, o4, m)
+    gpu.matvec(xq, wm, om, m)
+    orc.assert_close("mfma vs dot4", gpu.to_host(o4, m * n).astype(np.float64), gpu.to_host(om, m * n), 1e-5)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_mmq_many_targets(mfma, orc, m):
+    """Three weights of one type in one launch (MvTargets), tile counts 2, 4 and 19."""
+    t, k = 12, 2048
+    ns = [17, 64, 300]
+    ws = [make_weight(orc, t, n, k, 40 + i, "random") for i, n in enumerate(ns)]
+    wgs = [upload(mfma, t, w, n, k) for w, n in zip(ws, ns)]
+    x = orc.normal(9, m * k, 0.0, 1.0)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    outs = [mfma.alloc(m * n) for n in ns]
+    mfma.matvec_many(q8_1_to_device(mfma, qs, d, s), wgs, outs, m)
+    for w, n, o in zip(ws, ns, outs):
+        orc.assert_close(f"target {n}", orc.matvec_q8_1(t, w, n, k, qs, d, m), mfma.to_host(o, m * n), TOL_B)
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_matmul_many_mixed_families(gpu, orc, m):
+    """Backend::matmul_many over weights of both layouts: runs split where the family changes."""
+    k = 1024
+    spec = [(12, 64, "dot4"), (12, 48, "mfma"), (12, 16, "mfma"), (8, 40, "dot4"), (8, 24, "mfma"), (2, 56, "mfma")]
+    ws, wgs, outs = [], [], []
+    for i, (t, n, fam) in enumerate(spec):
+        gpu.set_kernels(fam)
+        w = make_weight(orc, t, n, k, 800 + i, "random")
+        ws.append(w)
+        wgs.append(upload(gpu, t, w, n, k))
+        outs.append(gpu.alloc(m * n))
+    gpu.set_kernels("auto")
+    x = orc.normal(801, m * k, 0.0, 1.0)
+    gpu.matmul_many(gpu.from_host(x), wgs, outs, m)
+    qs, d, _ = orc.quantize_q8_1(x, m, k)
+    for (t, n, fam), w, o in zip(spec, ws, outs):
+        orc.assert_close(f"{fam} type {t}", orc.matvec_q8_1(t, w, n, k, qs, d, m), gpu.to_host(o, m * n), TOL_B)
+
+
+def test_mixed_families_in_one_launch_is_an_error(gpu, orc):
+    from rllm_amd.errors import ShapeError
+
+    t, n, k = 12, 16, 512
+    w = make_weight(orc, t, n, k, 1, "random")
+    gpu.set_kernels("dot4")
+    a = upload(gpu, t, w, n, k)
+    gpu.set_kernels("mfma")
+    b = upload(gpu, t, w, n, k)
+    gpu.set_kernels("auto")
+    qs, d, s = orc.quantize_q8_1(orc.normal(2, k, 0.0, 1.0), 1, k)
+    with pytest.raises(ShapeError, match="different kernel families"):
+        gpu.matvec_many(q8_1_to_device(gpu, qs, d, s), [a, b], [gpu.alloc(n), gpu.alloc(n)], 1)
