@@ -61,6 +61,9 @@ _SIGNATURES = {
     "rq_reserve": (_int, [_vp, _i64]),
     "rq_block_dots": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
     "rq_set_kernels": (_int, [_vp, _int]),
+    "rq_act_mul": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(Q8_1Struct)]),
+    "rq_glu_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _i64, _vp, _i64]),
+    "rq_gated_ffn": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64, _vp, _i64, _vp, _i64]),
     "rq_weight_kernels": (_int, [_vp, ctypes.POINTER(_int)]),
 }
 

@@ -178,3 +178,38 @@ struct RqMmqRepackParams {
     int64_t rows;
     int32_t S2, k, pad[2];
 };
+
+// ---------------------------------------------------------------------------
+// Gated FFN front half (rq_glu_* in rq_kernels.hip, dot4 layout):
+// h[j][r] = act(gate_r . x_j) * (up_r . x_j), one workgroup per 32 rows r.
+
+#define RQ_ACT_SILU 0
+#define RQ_ACT_GELU_TANH 1
+
+struct RqGluParams {
+    RqTiled gate, up;    // same type, shape and tiling
+    const int8_t* xq;    // Q8_1 activations (rq_glu_*), column j at xq + j * k
+    const uint16_t* xd;
+    const float* xf;     // f32 activations (rq_gluf_*), one column
+    float* hf;           // f32 product h[j * n + r], or null
+    int8_t* hq;          // Q8_1 of h (column j at hq + j * n), or null
+    uint16_t* hd;
+    uint16_t* hs;
+    int32_t n;           // rows (multiple of 32)
+    int32_t m;           // activation columns of this launch
+    int32_t act;         // RQ_ACT_*
+    int32_t pad;
+};
+
+// Elementwise h = act(g) * u over len values (rq_act_mul), optionally Q8_1(h)
+// per 32 consecutive values.
+struct RqActParams {
+    float* g;            // in: gate values; out: h
+    const float* u;
+    int8_t* hq;          // or null
+    uint16_t* hd;
+    uint16_t* hs;
+    int64_t nblocks;     // len / 32
+    int32_t act;
+    int32_t pad;
+};
