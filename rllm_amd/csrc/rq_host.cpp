@@ -140,6 +140,7 @@ struct rq_ctx {
     hipFunction_t mmq[RQ_NUM_FMTS][4][3] = {};
     hipFunction_t mmqf[RQ_NUM_FMTS][3] = {};
     hipFunction_t mmqd[RQ_NUM_FMTS][4][3] = {};
+    hipFunction_t mmqg[RQ_NUM_FMTS][2][3] = {};  // 8 x G columns, G = 2, 4
     hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
@@ -380,13 +381,18 @@ bool mmq_supported(int fmt, int64_t cols) {
     return (mmq_S2(cols) + maxs - 1) / maxs <= 16;
 }
 
+// Columns per launch: up to 8 in one staged group (mp = 1, 2, 4, 8), or 8 x g
+// (g = 2, 4) staged one group after another against weights read once.
+constexpr int kMmqMaxCols = 32;
+
 struct MmqPlan {
-    int mp, sbw, ks, tr;
+    int mp, g, sbw, ks, tr;
     int kxp, z_off, pl_off, part_off, lds;
 };
 
-hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int sbw, bool f32_in, bool dots) {
+hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int g, int sbw, bool f32_in, bool dots) {
     const int si = mmq_sbw_index(sbw), mi = mmq_mp_index(mp);
+    if (g > 1) return ctx->mmqg[fmt][g == 2 ? 0 : 1][si];
     return f32_in ? ctx->mmqf[fmt][si] : dots ? ctx->mmqd[fmt][mi][si] : ctx->mmq[fmt][mi][si];
 }
 
@@ -396,35 +402,46 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
     L.z_off = L.mp * L.kxp;
     L.pl_off = L.z_off + L.sbw * 256;
     L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * NB * 4;
-    L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * 4);
+    L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4);
 }
 
 // Launch geometry and LDS layout of an rq_mmq launch over weights of S2
 // super-blocks per row and `tiles` tiles in total.
 //   sbw: the fewest super-blocks per wave that keep a tile's k-parts within
-//        one workgroup, raised from 2 to 4 when that still leaves >= 2048
-//        waves (fewer, longer waves stage and reduce less); RQ_MMQ_SBW overrides.
+//        one workgroup (shorter waves finish sooner after their last weight
+//        load: fastest for 1 to 4 columns at 14336 x 4096); RQ_MMQ_SBW
+//        overrides.
 //   tr:  tiles per workgroup, the smallest that lets every workgroup be
 //        resident at once (per HIP's occupancy for the kernel's registers and
 //        LDS), else the one with the fewest rounds; RQ_MMQ_TR overrides.
-MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int64_t tiles, bool f32_in, bool dots) {
+// Launches of 8 or more columns instead stage 8 columns per workgroup per
+// group, which costs as much as the weights' arithmetic: they take sbw >= 4
+// and the most tiles per workgroup that fit (16 waves), so each staging
+// serves 4 tiles (measured at 14336 x 4096: 11.8 / 17.9 / 29.5 us for 8 / 16
+// / 32 columns against 12.2 / 21.6 / 39.4 with sbw 2 and one tile).
+MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int g, int64_t tiles, bool f32_in, bool dots) {
     MmqPlan L;
     L.mp = mp;
+    L.g = g;
     const int maxs = mmq_sbw_max(fmt);
     int sbw = 2;
     while (sbw < maxs && (S2 + sbw - 1) / sbw > 16) sbw *= 2;
     if (ctx->mmq_sbw >= sbw && ctx->mmq_sbw <= maxs && (ctx->mmq_sbw & (ctx->mmq_sbw - 1)) == 0)
         sbw = ctx->mmq_sbw;
-    else if (sbw == 2 && tiles * ((S2 + 3) / 4) >= 2048)
-        sbw = 4;
+    else if (mp == 8 && !dots)
+        sbw = std::max(sbw, std::min(4, maxs));
     L.sbw = sbw;
     L.ks = (S2 + sbw - 1) / sbw;
-    if (ctx->mmq_tr > 0) {
-        L.tr = std::max(1, std::min(ctx->mmq_tr, 16 / L.ks));
+    if (ctx->mmq_tr > 0 || (mp == 8 && !dots)) {
+        L.tr = std::max(1, std::min(ctx->mmq_tr > 0 ? ctx->mmq_tr : 16, 16 / L.ks));
         mmq_layout(fmt, S2, dots, L);
+        while (L.tr > 1 && L.lds > ctx->lds_wide) {
+            L.tr /= 2;
+            mmq_layout(fmt, S2, dots, L);
+        }
         return L;
     }
-    hipFunction_t f = mmq_kernel(ctx, fmt, mp, sbw, f32_in, dots);
+    hipFunction_t f = mmq_kernel(ctx, fmt, mp, g, sbw, f32_in, dots);
     int64_t best_rounds = -1;
     MmqPlan best = L;
     for (int tr = 1; tr * L.ks <= 16; tr *= 2) {
@@ -457,11 +474,19 @@ int pow2_at_least(int v) {
     return p;
 }
 
+// Column grouping of an MFMA launch of nc columns: mp (columns staged at
+// once) and g (groups of 8 staged in turn).
+void mmq_cols(int nc, int& mp, int& g) {
+    mp = nc <= 8 ? pow2_at_least(nc) : 8;
+    g = nc <= 8 ? 1 : (nc <= 16 ? 2 : 4);
+}
+
 // MFMA matvec / block-dot launches over `count` same-type weights of width k.
-// The m columns run in the fewest near-equal groups of <= 8 whose staging fits
-// the LDS a workgroup may use; every launch reads the weights once. xf set:
-// one f32 column quantized while staging (rq_mmqf_*); dots set: int32 block
-// dots instead of the f32 sums (rq_mmqd_*; `outs` are then int32 arrays).
+// The m columns run in the fewest near-equal launches of <= 32 (block dots:
+// <= 8) whose staging fits the LDS a workgroup may use; every launch reads
+// the weights once. xf set: one f32 column quantized while staging
+// (rq_mmqf_*); dots set: int32 block dots instead of the f32 sums (rq_mmqd_*;
+// `outs` are then int32 arrays).
 rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
                      const rq_weight* const* ws, void* const* outs, int count, bool dots) {
     const int fmt = ws[0]->fmt;
@@ -469,19 +494,23 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     const int S2 = ws[0]->S2;
     int64_t tiles = 0;
     for (int i = 0; i < count; i++) tiles += ws[i]->tiles;
-    int64_t ngroups = (m + 7) / 8;
-    MmqPlan L;
+    const int max_cols = (xf || dots) ? (xf ? 1 : 8) : kMmqMaxCols;
+    int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         const int nc = (int)((m + ngroups - 1) / ngroups);
-        L = mmq_plan(ctx, fmt, S2, xf ? 1 : pow2_at_least(nc), tiles, xf != nullptr, dots);
+        int mp, g;
+        mmq_cols(nc, mp, g);
+        const MmqPlan L = mmq_plan(ctx, fmt, S2, mp, g, tiles, xf != nullptr, dots);
         if (L.lds <= ctx->lds_wide) break;
         if (nc == 1)
             return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage (%d bytes of LDS)", (long long)k, L.lds);
-        ngroups = (m + nc / 2 - 1) / (nc / 2);
+        ngroups++;
     }
     for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
         const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
-        const MmqPlan P = mmq_plan(ctx, fmt, S2, xf ? 1 : pow2_at_least(nc), tiles, xf != nullptr, dots);
+        int mp, g;
+        mmq_cols(nc, mp, g);
+        const MmqPlan P = mmq_plan(ctx, fmt, S2, mp, g, tiles, xf != nullptr, dots);
         RqMmqParams p;
         memset(&p, 0, sizeof p);
         int64_t wgs = 0;
@@ -511,8 +540,9 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
         p.z_off = P.z_off;
         p.pl_off = P.pl_off;
         p.part_off = P.part_off;
-        hipFunction_t f = mmq_kernel(ctx, fmt, P.mp, P.sbw, xf != nullptr, dots);
-        if (!f) return fail(RQ_ERR_UNSUPPORTED, "matvec: no MFMA kernel for %d columns, %d super-blocks per wave", P.mp, P.sbw);
+        hipFunction_t f = mmq_kernel(ctx, fmt, P.mp, P.g, P.sbw, xf != nullptr, dots);
+        if (!f) return fail(RQ_ERR_UNSUPPORTED, "matvec: no MFMA kernel for %d x %d columns, %d super-blocks per wave",
+                            P.mp, P.g, P.sbw);
         rq_status st = launch(ctx, f, dots ? "rq_mmqd" : xf ? "rq_mmqf" : "rq_mmq", (uint64_t)wgs, &p, (unsigned)P.lds,
                               (unsigned)(64 * P.ks * P.tr));
         if (st != RQ_OK) return st;
@@ -647,6 +677,10 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
             if (kMmqSbw[si] > mmq_sbw_max(f)) continue;
             snprintf(name, sizeof name, "rq_mmqf_%s_%d", kFmtSuffix[f], kMmqSbw[si]);
             st = getm(ctx->mmq_mod, &ctx->mmqf[f][si], name);
+            for (int gi = 0; gi < 2 && st == RQ_OK; gi++) {
+                snprintf(name, sizeof name, "rq_mmq_%s_8x%d_%d", kFmtSuffix[f], gi == 0 ? 2 : 4, kMmqSbw[si]);
+                st = getm(ctx->mmq_mod, &ctx->mmqg[f][gi][si], name);
+            }
             for (int mi = 0; mi < 4 && st == RQ_OK; mi++) {
                 snprintf(name, sizeof name, "rq_mmq_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
                 if ((st = getm(ctx->mmq_mod, &ctx->mmq[f][mi][si], name)) != RQ_OK) break;

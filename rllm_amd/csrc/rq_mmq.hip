@@ -2,6 +2,7 @@
 // layout documented in rq_params.h.
 //
 //   rq_mmq_<fmt>_<mp>_<sbw>  Q8_1 activations, up to mp = 1, 2, 4, 8 columns
+//   rq_mmq_<fmt>_8x<g>_<sbw> up to 8 g columns (g = 2, 4 groups of 8, weights read once)
 //   rq_mmqf_<fmt>_<sbw>      one f32 activation column, quantized while staging
 //   rq_mmqd_<fmt>_<mp>_<sbw> the int32 block dots of the same MFMA path (debug)
 //   rq_mmq_repack_<fmt>      GGUF rows -> 16-row tiles (upload)
@@ -108,7 +109,7 @@ struct XB {
 
 __device__ __forceinline__ void xb_load(const RqMmqParams& P, int a, int b, XB& x) {
     const int U = P.k >> 5;
-    x.valid = a < P.m && b < U;
+    x.valid = a < P.m && b < U;  // a: the column within the launch
     const int ac = min(a, P.m - 1), bc = min(b, U - 1);
     const int4* p = (const int4*)(P.xq + (int64_t)ac * P.k + (int64_t)bc * 32);
     x.lo = p[0];
@@ -237,7 +238,10 @@ __device__ __forceinline__ Scales<FMT, MP> scales_of(const int4 h, bool hsel, in
 // ---------------------------------------------------------------------------
 // The matvec (and, with DOTS, the block-dot debug kernel).
 
-template <int FMT, int MP, int SBW, bool F32IN, bool DOTS>
+// G > 1 (mp = 8): the launch's columns come in G groups of 8 that are staged
+// and computed one after another through the same LDS, against weights loaded
+// once into registers.
+template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1>
 __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr bool NIB = MF<FMT>::NIB;
     constexpr int PS = 16 / MP;                // D rows (slots) per activation
@@ -277,7 +281,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     if (F32IN) {
         qf_load(P, tid >> 2, q0);
     } else {
-        xb_load(P, tid % MP, tid / MP, x0);  // item it = MP * block + column
+        xb_load(P, tid % MP, tid / MP, x0);  // item it = MP * block + column (group 0)
     }
     // Header i, then the code loads it scales (mp = 1: one D-group of two
     // super-blocks, of which the lane needs one header; mp >= 2: one
@@ -302,6 +306,17 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- Staging writes (the LDS writes wait only for the staging loads).
+    for (int i = tid; i < SBW * 16; i += threads) *(int4*)(mmq_lds + P.z_off + 16 * i) = make_int4(0, 0, 0, 0);
+    float y[G][NACC];
+#pragma unroll
+    for (int gi = 0; gi < G; gi++)
+#pragma unroll
+        for (int e = 0; e < NACC; e++) y[gi][e] = 0.f;
+
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+    const int col0 = gi * MP;  // first column of this group
+    if (gi > 0) __syncthreads();  // the previous group's LDS reads are done
     if (F32IN) {
         qf_write<FMT>(P, q0);
         for (int base = threads; base < 4 * NB; base += threads) {  // uniform trip count
@@ -310,19 +325,16 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
             qf_write<FMT>(P, q);
         }
     } else {
-        if (tid < MP * NB) xb_write<FMT, MP, DOTS>(P, tid % MP, tid / MP, x0);
-        for (int it = tid + threads; it < MP * NB; it += threads) {
+        if (gi == 0) {
+            if (tid < MP * NB) xb_write<FMT, MP, DOTS>(P, tid % MP, tid / MP, x0);
+        }
+        for (int it = tid + (gi == 0 ? threads : 0); it < MP * NB; it += threads) {
             XB x;
-            xb_load(P, it % MP, it / MP, x);
+            xb_load(P, col0 + it % MP, it / MP, x);
             xb_write<FMT, MP, DOTS>(P, it % MP, it / MP, x);
         }
     }
-    for (int i = tid; i < SBW * 16; i += threads) *(int4*)(mmq_lds + P.z_off + 16 * i) = make_int4(0, 0, 0, 0);
     __syncthreads();
-
-    float y[NACC];
-#pragma unroll
-    for (int e = 0; e < NACC; e++) y[e] = 0.f;
 
     if (has_tile) {
         // A operand: row ia = lane % 16 of A is (activation ia / PS, slot ia % PS);
@@ -413,20 +425,20 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                         accd = fmaf(byte_f(sc.sc, v), tv, accd);
                         accm = fmaf(byte_f(sc.mn, v), pv1[v], accm);
                     }
-                    y[0] = fmaf(sc.d, accd, y[0]);
-                    y[0] = fmaf(-sc.dmin, accm, y[0]);
+                    y[gi][0] = fmaf(sc.d, accd, y[gi][0]);
+                    y[gi][0] = fmaf(-sc.dmin, accm, y[gi][0]);
                 } else if (FMT == RQ_FMT_Q4_0) {
                     const float4 p1 = *(const float4*)(mmq_lds + pofs + stride);
                     const float pv1[4] = {p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         const float tv = fmaf(pv0[v], (float)D[v], pv1[v]);
-                        y[0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), tv, y[0]);
+                        y[gi][0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), tv, y[gi][0]);
                     }
                 } else {
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        y[0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), pv0[v] * (float)D[v], y[0]);
+                        y[gi][0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), pv0[v] * (float)D[v], y[gi][0]);
                 }
             } else {  // mp = 8: two activations per lane, blocks pb, pb + 1
 #pragma unroll
@@ -447,44 +459,48 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                             accd = fmaf(byte_f(sc.sc, bsh + h), tv, accd);
                             accm = fmaf(byte_f(sc.mn, bsh + h), pv1[h], accm);
                         }
-                        y[e] = fmaf(sc.d, accd, y[e]);
-                        y[e] = fmaf(-sc.dmin, accm, y[e]);
+                        y[gi][e] = fmaf(sc.d, accd, y[gi][e]);
+                        y[gi][e] = fmaf(-sc.dmin, accm, y[gi][e]);
                     } else if (FMT == RQ_FMT_Q4_0) {
                         const float2 p1 = *(const float2*)(mmq_lds + pofs + stride);
                         const float pv1[2] = {p1.x, p1.y};
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
                             const float tv = fmaf(pv0[h], (float)D[2 * e + h], pv1[h]);
-                            y[e] = fmaf(half_f(sc.dw0, h), tv, y[e]);
+                            y[gi][e] = fmaf(half_f(sc.dw0, h), tv, y[gi][e]);
                         }
                     } else {
 #pragma unroll
                         for (int h = 0; h < 2; h++)
-                            y[e] = fmaf(half_f(sc.dw0, h), pv0[h] * (float)D[2 * e + h], y[e]);
+                            y[gi][e] = fmaf(half_f(sc.dw0, h), pv0[h] * (float)D[2 * e + h], y[gi][e]);
                     }
                 }
             }
         }
     }
+    }  // column groups
     if (DOTS) return;
 
     // ---- Partial sums of the k-parts and k-group lanes, in a fixed order:
     // first the lanes of one (row, activation) within the wave (mp = 1: four
     // k-groups, mp = 2: two), then the k-parts in LDS.
-    if (MP <= 2) y[0] += __shfl_xor(y[0], 16);
-    if (MP == 1) y[0] += __shfl_xor(y[0], 32);
+    if (MP <= 2) y[0][0] += __shfl_xor(y[0][0], 16);
+    if (MP == 1) y[0][0] += __shfl_xor(y[0][0], 32);
     float* part = (float*)(mmq_lds + P.part_off);
 #pragma unroll
-    for (int e = 0; e < NACC; e++) part[(wave * 64 + lane) * NACC + e] = y[e];
+    for (int gi = 0; gi < G; gi++)
+#pragma unroll
+        for (int e = 0; e < NACC; e++) part[((wave * G + gi) * 64 + lane) * NACC + e] = y[gi][e];
     __syncthreads();
     float* out = (float*)T.out;
-    for (int it = tid; it < P.tr * MP * 16; it += threads) {
-        const int tl2 = it / (MP * 16), a = (it >> 4) % MP, nn = it & 15;
+    for (int it = tid; it < P.tr * G * MP * 16; it += threads) {
+        const int tl2 = it / (G * MP * 16), ag = (it >> 4) % (G * MP), nn = it & 15;
+        const int gi = ag / MP, a = ag % MP;
         const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn;
-        if (a >= P.m || tile2 >= T.tiles || row >= T.n) continue;
+        if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
         float s = 0.f;
         for (int q = 0; q < ks; q++) {
-            const int w = tl2 * ks + q;
+            const int w = (tl2 * ks + q) * G + gi;
             if (MP == 1) {
                 s += part[w * 64 + nn];
             } else if (MP == 2) {
@@ -495,7 +511,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                 s += part[(w * 64 + 16 * (a >> 1) + nn) * 2 + (a & 1)];
             }
         }
-        out[(int64_t)a * T.n + row] = s;
+        out[(int64_t)ag * T.n + row] = s;
     }
 }
 
@@ -506,11 +522,17 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     extern "C" __global__ __launch_bounds__(1024) void rq_mmqd_##NAME##_##MP##_##SBW(RqMmqParams p) { \
         mmq_body<FMT, MP, SBW, false, true>(p);                                                     \
     }
+#define RQ_MMQ_G(NAME, FMT, G, SBW)                                                                      \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_##NAME##_8x##G##_##SBW(RqMmqParams p) {       \
+        mmq_body<FMT, 8, SBW, false, false, G>(p);                                                          \
+    }
 #define RQ_MMQ_SET(NAME, FMT, SBW)                                                               \
     RQ_MMQ(NAME, FMT, 1, SBW)                                                                    \
     RQ_MMQ(NAME, FMT, 2, SBW)                                                                    \
     RQ_MMQ(NAME, FMT, 4, SBW)                                                                    \
     RQ_MMQ(NAME, FMT, 8, SBW)                                                                    \
+    RQ_MMQ_G(NAME, FMT, 2, SBW)                                                                  \
+    RQ_MMQ_G(NAME, FMT, 4, SBW)                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void rq_mmqf_##NAME##_##SBW(RqMmqParams p) {     \
         mmq_body<FMT, 1, SBW, true, false>(p);                                                   \
     }
