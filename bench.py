@@ -293,8 +293,8 @@ def main() -> int:
         return 2
     traffic = None if args.no_traffic else measure_traffic()
     if traffic:
-        log(f"traffic: {traffic['bytes'] / 1e6:.2f} MB per launch (fetch x{traffic['fetch_scale']:.4f}, "
-            f"write x{traffic['write_scale']:.4f})")
+        log(f"traffic: {traffic['bytes'] / 1e6:.2f} MB per launch: fetch {traffic['fetch']:.0f} B "
+            f"(x{traffic['fetch_scale']:.4f}), write {traffic['write']:.0f} B (x{traffic['write_scale']:.4f})")
 
     import torch
 
@@ -361,6 +361,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,
+                     "traffic_fetch": round(traffic["fetch"]) if traffic else None,
+                     "traffic_write": round(traffic["write"]) if traffic else None,
                      "kernel": KERNEL_PREFIX[r["kernels"]] + ("*" if r["kernels"] == "mfma" else ""),
                      "kernel_us": round(r["us"], 3), "alg_bytes": r["bytes"]},
         "cpu_baseline": cpu,
