@@ -65,6 +65,9 @@ _SIGNATURES = {
     "rq_glu_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _i64, _vp, _i64]),
     "rq_gated_ffn": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64, _vp, _i64, _vp, _i64]),
     "rq_weight_kernels": (_int, [_vp, ctypes.POINTER(_int)]),
+    "rq_rms_norm": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, ctypes.c_float, ctypes.POINTER(Q8_1Struct)]),
+    "rq_add_rms_norm": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, ctypes.c_float,
+                               ctypes.POINTER(Q8_1Struct)]),
 }
 
 _lib: ctypes.CDLL | None = None

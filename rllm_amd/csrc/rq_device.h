@@ -15,6 +15,17 @@ __device__ __forceinline__ float h2f(u32 h) { return (float)__builtin_bit_cast(_
 // f32 -> f16 with v_cvt_f16_f32 (round to nearest even).
 __device__ __forceinline__ u16 f2h(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
 
+// f16 of the f32 product a * b: rounded twice, to f32 and then to f16, as the
+// Q8_1 sum field is defined. The empty asm makes the f32 product a value the
+// compiler cannot see through; otherwise it fuses the multiply into the
+// conversion (v_fma_mixlo_f16 rounds the exact product once, which differs
+// when the f32 product is an exact f16 tie), with or without contraction.
+__device__ __forceinline__ u16 f2h_mul(float a, float b) {
+    float p = a * b;
+    __asm__ volatile("" : "+v"(p));
+    return f2h(p);
+}
+
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);

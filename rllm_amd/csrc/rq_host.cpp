@@ -128,6 +128,7 @@ struct rq_ctx {
     hipFunction_t glu[RQ_NUM_FMTS][RQ_MV_MAX_NC + 1] = {};  // gated FFN front half, Q8_1 x
     hipFunction_t gluf[RQ_NUM_FMTS] = {};                   // the same from one f32 column
     hipFunction_t act_mul = nullptr;
+    hipFunction_t norm[4] = {};  // rq_rms_norm_<vpt>, vpt = 1, 2, 4, 8
     // Q8_1 of the gated FFN's product h (rq_gated_ffn), grown like sq/sd/ss.
     int8_t* hq = nullptr;
     uint16_t* hd = nullptr;
@@ -645,6 +646,11 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     };
     rq_status st = get(&ctx->quant, "rq_quantize_q8_1");
     if (st == RQ_OK) st = get(&ctx->act_mul, "rq_act_mul");
+    for (int i = 0; i < 4 && st == RQ_OK; i++) {
+        char nname[32];
+        snprintf(nname, sizeof nname, "rq_rms_norm_%d", 1 << i);
+        st = get(&ctx->norm[i], nname);
+    }
     char name[64];
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
         for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {
@@ -1182,6 +1188,78 @@ extern "C" rq_status rq_act_mul(rq_ctx* ctx, int act, float* gate, int64_t gate_
     if (hq && !hq->s) return fail(RQ_ERR_INVALID, "%s: null Q8_1 s", act_name(act));
     if ((st = bind(ctx)) != RQ_OK) return st;
     return act_mul_launch(ctx, act, gate, up, len, hq ? hq->qs : nullptr, hq ? hq->d : nullptr, hq ? hq->s : nullptr);
+}
+
+// RMS norm launch over `rows` rows of width d (d % 4 == 0, d <= 32768):
+// one workgroup per row, pow2 threads (64..1024) holding vpt float4s each.
+static rq_status norm_run(rq_ctx* ctx, const char* what, float* x, const float* y, const float* w, float* out, int64_t rows,
+                          int64_t d, float eps, const rq_q8_1* qout) {
+    const int64_t nv = d / 4;
+    int threads = 64;
+    while (threads < 1024 && threads < nv) threads *= 2;
+    int vi = 0;
+    while (vi < 3 && (int64_t)threads * (1 << vi) < nv) vi++;
+    RqNormParams p;
+    memset(&p, 0, sizeof p);
+    p.x = x;
+    p.y = y;
+    p.w = w;
+    p.out = out;
+    if (qout) {
+        p.hq = qout->qs;
+        p.hd = qout->d;
+        p.hs = qout->s;
+    }
+    p.d = (int32_t)d;
+    p.eps = eps;
+    return launch(ctx, ctx->norm[vi], what, (uint64_t)rows, &p, 0, (unsigned)threads);
+}
+
+// Shared argument checks of rq_rms_norm and rq_add_rms_norm.
+static rq_status check_norm(const char* what, const void* x, const void* y, const float* w, int64_t d, const float* out,
+                            int64_t rows, const rq_q8_1* qout) {
+    if (rows < 0) return fail(RQ_ERR_SHAPE, "%s: negative row count %lld", what, (long long)rows);
+    if (d <= 0 || d % 4 != 0 || d > (int64_t)RQ_NORM_MAX_VPT * 4 * 1024)
+        return fail(RQ_ERR_SHAPE, "%s: width %lld must be a positive multiple of 4 up to %d", what, (long long)d,
+                    RQ_NORM_MAX_VPT * 4 * 1024);
+    if (!x || !w || !out || (y && !aligned(y, 16)) || !aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))
+        return fail(RQ_ERR_INVALID, "%s: buffers must be 16-byte aligned pointers", what);
+    if (qout) {
+        if (d % 32 != 0)
+            return fail(RQ_ERR_SHAPE, "%s: Q8_1 output needs a width that is a multiple of 32, got %lld", what,
+                        (long long)d);
+        rq_status st = check_q8_1(what, qout, rows * d);
+        if (st != RQ_OK) return st;
+        if (!qout->s) return fail(RQ_ERR_INVALID, "%s: null Q8_1 s", what);
+    }
+    return RQ_OK;
+}
+
+extern "C" rq_status rq_rms_norm(rq_ctx* ctx, const float* x, int64_t x_len, const float* w, int64_t w_len,
+                                 float* out, int64_t out_len, int64_t rows, float eps, const rq_q8_1* qout) {
+    if (!ctx) return fail(RQ_ERR_INVALID, "rms_norm: null context");
+    const int64_t d = w_len;
+    rq_status st = check_len("rms_norm x", x_len, rows * d);
+    if (st != RQ_OK || (st = check_len("rms_norm out", out_len, rows * d)) != RQ_OK) return st;
+    if ((st = check_norm("rms_norm", x, nullptr, w, d, out, rows, qout)) != RQ_OK) return st;
+    if (rows == 0) return RQ_OK;
+    if ((st = bind(ctx)) != RQ_OK) return st;
+    return norm_run(ctx, "rq_rms_norm", const_cast<float*>(x), nullptr, w, out, rows, d, eps, qout);
+}
+
+extern "C" rq_status rq_add_rms_norm(rq_ctx* ctx, float* x, int64_t x_len, const float* y, int64_t y_len,
+                                     const float* w, int64_t w_len, float* out, int64_t out_len, int64_t rows,
+                                     int64_t width, float eps, const rq_q8_1* qout) {
+    if (!ctx) return fail(RQ_ERR_INVALID, "add_rms_norm: null context");
+    rq_status st = check_len("add_rms_norm weight", w_len, width);
+    if (st != RQ_OK || (st = check_len("add_rms_norm x", std::min(x_len, y_len), rows * width)) != RQ_OK ||
+        (st = check_len("add_rms_norm out", out_len, rows * width)) != RQ_OK)
+        return st;
+    if (!y) return fail(RQ_ERR_INVALID, "add_rms_norm: null y");
+    if ((st = check_norm("add_rms_norm", x, y, w, width, out, rows, qout)) != RQ_OK) return st;
+    if (rows == 0) return RQ_OK;
+    if ((st = bind(ctx)) != RQ_OK) return st;
+    return norm_run(ctx, "rq_add_rms_norm", x, y, w, out, rows, width, eps, qout);
 }
 
 extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* gate,

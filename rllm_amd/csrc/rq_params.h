@@ -201,6 +201,22 @@ struct RqGluParams {
     int32_t pad;
 };
 
+// RMS norm of rows of width d (rq_rms_norm, rq_add_rms_norm): per row,
+// [x += y;] out = x * (1 / sqrt(sum(x^2) / d + eps)) * w, optionally with
+// Q8_1(out) per 32 consecutive values (d % 32 == 0). One workgroup per row.
+#define RQ_NORM_MAX_VPT 8  // float4s per thread: d <= 8 * 4 * 1024
+struct RqNormParams {
+    float* x;            // [rows, d]; x + y is written back when y is set
+    const float* y;      // or null
+    const float* w;      // [d]
+    float* out;          // [rows, d]
+    int8_t* hq;          // Q8_1 of out, or null
+    uint16_t* hd;
+    uint16_t* hs;
+    int32_t d;
+    float eps;
+};
+
 // Elementwise h = act(g) * u over len values (rq_act_mul), optionally Q8_1(h)
 // per 32 consecutive values.
 struct RqActParams {

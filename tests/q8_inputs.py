@@ -23,3 +23,26 @@ def near_tie_rows(m: int, k: int, seed: int) -> np.ndarray:
         v = np.where(steps <= -s, np.nextafter(v, np.float32(-np.inf)), v)
     v = np.clip(v, -amax[:, None], amax[:, None]).astype(np.float32)
     return np.concatenate([amax[:, None], v], axis=1).reshape(m, k).astype(np.float32)
+
+
+def s16_tie_blocks(nblocks: int, seed: int) -> np.ndarray:
+    """Blocks whose Q8_1 sum field is an f16 rounding tie after the f32 product.
+
+    s16 = f16(f32(d * S)) rounds twice. When f32(d * S) lands exactly halfway
+    between two f16 values while the exact product d * S does not, rounding
+    the exact product once (a fused multiply-convert) picks the other f16
+    value. Returns [nblocks, 32] f32 blocks (searched among N(0, 1) blocks
+    with numpy's IEEE float32 arithmetic) where the two roundings differ.
+    """
+    rng = np.random.default_rng(seed)
+    found = []
+    while sum(len(f) for f in found) < nblocks:
+        x = rng.standard_normal((1 << 18, 32)).astype(np.float32)
+        amax = np.max(np.abs(x), axis=1)
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        q = np.rint(x / d[:, None]).astype(np.float32)
+        S = np.sum(q, axis=1, dtype=np.float64).astype(np.float32)
+        twice = (d * S).astype(np.float32).astype(np.float16)
+        once = (d.astype(np.float64) * S.astype(np.float64)).astype(np.float16)
+        found.append(x[twice != once])
+    return np.concatenate(found)[:nblocks]

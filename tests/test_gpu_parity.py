@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from gpu_util import make_weight, q8_1_to_device, upload
-from q8_inputs import near_tie_rows
+from q8_inputs import near_tie_rows, s16_tie_blocks
 from rllm_amd.errors import ShapeError, UnsupportedError
 
 pytestmark = pytest.mark.gpu
@@ -77,6 +77,18 @@ def test_quantize_q8_1_near_ties(gpu, orc, m, k):
     assert bad.size == 0, f"{bad.size} codes differ, first at {bad[:4]}: x={x.reshape(-1)[bad[:4]]}"
     assert np.array_equal(gd, od)
     assert np.array_equal(gs, os_)
+
+
+def test_quantize_q8_1_s16_ties(gpu, orc):
+    """Blocks where f32(d * S) is an exact f16 tie: the sum field must be
+    rounded twice (f32, then f16), not fused into one rounding."""
+    x = s16_tie_blocks(64, 5).reshape(-1)
+    m, k = 2, 1024
+    gq, gd, gs = gpu.quantize_q8_1(gpu.from_host(x), m, k).to_host()
+    oq, od, os_ = orc.quantize_q8_1(x, m, k)
+    assert np.array_equal(gq, oq) and np.array_equal(gd, od)
+    bad = np.flatnonzero(gs != os_)
+    assert bad.size == 0, f"s16 differs in {bad.size} of 64 tie blocks: {[hex(v) for v in gs[bad[:4]]]}"
 
 
 # ---- block dots (bit-exact) -------------------------------------------------
