@@ -142,13 +142,19 @@ def bench_decode(torch, gpu, orc, replays):
 
     t0 = time.time()
     host = {name: make_gguf(orc, t, n, k, 100 + i) for i, (name, t, n, k) in enumerate(LAYER)}
+    head_bytes = make_gguf(orc, HEAD[1], HEAD[2], HEAD[3], 999, "random")
+    # Model load: every weight through rq_upload (host memory -> pinned
+    # staging -> device repack), timed as a whole.
+    t1 = time.perf_counter()
     layers = []
     for _ in range(N_LAYERS):
         layers.append({name: gpu.upload(HostTensor(name, DType(t), (n, k), host[name])) for name, t, n, k in LAYER})
-    head_bytes = make_gguf(orc, HEAD[1], HEAD[2], HEAD[3], 999, "random")
     head = gpu.upload(HostTensor("output", DType(HEAD[1]), (HEAD[2], HEAD[3]), head_bytes))
+    up_s = time.perf_counter() - t1
+    up_bytes = sum(host[name].nbytes for name, _, _, _ in LAYER) * N_LAYERS + head_bytes.nbytes
     del host, head_bytes
-    log(f"decode weights uploaded in {time.time() - t0:.1f} s")
+    log(f"decode weights built and uploaded in {time.time() - t0:.1f} s "
+        f"(upload {up_bytes / 1e9:.2f} GB in {up_s * 1e3:.0f} ms = {up_bytes / up_s / 1e9:.1f} GB/s)")
     from rllm_amd.backend import Activation
 
     x = gpu.from_host(orc.normal(5, 4096))
@@ -182,7 +188,8 @@ def bench_decode(torch, gpu, orc, replays):
             w.free()
     head.free()
     torch.cuda.synchronize()
-    return {"us": us, "tok_s": 1e6 / us, "bytes": per_step, "gbs": per_step / us / 1e3}
+    return {"us": us, "tok_s": 1e6 / us, "bytes": per_step, "gbs": per_step / us / 1e3,
+            "upload_gbs": up_bytes / up_s / 1e9}
 
 
 def cpu_baseline(orc, t, n, k, reps=5):
@@ -358,6 +365,7 @@ def main() -> int:
         "pct_hbm_peak": round(100 * r["gbs"] / HBM_PEAK_GBS, 2),
         "decode_tok_s": round(dec["tok_s"], 1) if dec else None,
         "decode_step_us": round(dec["us"], 1) if dec else None,
+        "upload_gbs": round(dec["upload_gbs"], 1) if dec else None,
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": round(traffic["bytes"]) if traffic else None,

@@ -13,13 +13,13 @@ import re
 
 import torch  # noqa: F401  (loads the process's HIP runtime first)
 
-from .errors import BackendError, RllmError, ShapeError, UnsupportedError
+from .errors import BackendError, GgufError, RllmError, ShapeError, UnsupportedError
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "lib", "librq.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "rq.h")
 
-RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID = 0, 1, 2, 3, 4
+RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID, RQ_ERR_GGUF = 0, 1, 2, 3, 4, 5
 MATVEC_MAX_COLS = 8
 # Kernel families (rq_set_kernels).
 KERNELS_AUTO, KERNELS_DOT4, KERNELS_MFMA = 0, 1, 2
@@ -32,6 +32,33 @@ class Q8_1Struct(ctypes.Structure):
         ("d", ctypes.c_void_p),
         ("s", ctypes.c_void_p),
         ("len", ctypes.c_int64),
+    ]
+
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_void_p),
+        ("name_len", ctypes.c_uint64),
+        ("type", ctypes.c_int32),
+        ("n_dims", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * 8),
+        ("offset", ctypes.c_uint64),
+        ("size", ctypes.c_uint64),
+        ("data", ctypes.c_void_p),
+    ]
+
+
+class GgufValue(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("item_type", ctypes.c_uint32),
+        ("u64", ctypes.c_uint64),
+        ("i64", ctypes.c_int64),
+        ("f64", ctypes.c_double),
+        ("str", ctypes.c_void_p),
+        ("len", ctypes.c_uint64),
+        ("offset", ctypes.c_uint64),
+        ("items", ctypes.c_int64),
     ]
 
 
@@ -65,6 +92,17 @@ _SIGNATURES = {
     "rq_glu_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _i64, _vp, _i64]),
     "rq_gated_ffn": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64, _vp, _i64, _vp, _i64]),
     "rq_weight_kernels": (_int, [_vp, ctypes.POINTER(_int)]),
+    "rq_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "rq_gguf_close": (_int, [_vp]),
+    "rq_gguf_header": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                              ctypes.POINTER(ctypes.c_uint64)]),
+    "rq_gguf_tensor": (_int, [_vp, _i64, ctypes.POINTER(GgufTensorInfo)]),
+    "rq_gguf_find_tensor": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_i64)]),
+    "rq_gguf_meta": (_int, [_vp, _i64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64),
+                            ctypes.POINTER(GgufValue)]),
+    "rq_gguf_find_meta": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(GgufValue)]),
+    "rq_gguf_array_item": (_int, [_vp, ctypes.POINTER(GgufValue), ctypes.c_uint64, ctypes.POINTER(GgufValue)]),
+    "rq_gguf_upload": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "rq_rms_norm": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, ctypes.c_float, ctypes.POINTER(Q8_1Struct)]),
     "rq_add_rms_norm": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, ctypes.c_float,
                                ctypes.POINTER(Q8_1Struct)]),
@@ -109,4 +147,6 @@ def check(status: int) -> None:
         raise UnsupportedError(msg)
     if status == RQ_ERR_BACKEND:
         raise BackendError(msg)
+    if status == RQ_ERR_GGUF:
+        raise GgufError(msg)
     raise RllmError(f"invalid argument: {msg}")

@@ -201,6 +201,16 @@ class HipBackend:
         _lib.check(_lib.lib().rq_upload(self.ctx, int(dtype), rows, cols, data.ctypes.data, data.nbytes, ctypes.byref(h)))
         return HipWeight(self, h.value, dtype, rows, cols, t.name)
 
+    def upload_gguf(self, g, name: str) -> HipWeight:
+        """load_weight + Backend::upload of a named 2-D quantized tensor straight
+        from a mapped GGUF file (`rllm_amd.gguf.GgufFile`; rq_gguf_upload)."""
+        info = g.require_tensor(name)
+        dtype = DType.from_ggml(info.type)
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().rq_gguf_upload(self.ctx, g.handle, name.encode(), ctypes.byref(h)))
+        rows, cols = (info.dims[1], info.dims[0]) if len(info.dims) == 2 else (0, 0)
+        return HipWeight(self, h.value, dtype, rows, cols, name)
+
     def weight_to_gguf(self, w: HipWeight) -> np.ndarray:
         out = np.empty(w.rows * w.dtype.row_bytes(w.cols), dtype=np.uint8)
         _lib.check(_lib.lib().rq_weight_to_gguf(self.ctx, w.handle, out.ctypes.data, out.nbytes))

@@ -74,7 +74,7 @@ def build(verbose: bool = False) -> str:
     _run([
         "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{CSRC}",
-        os.path.join(CSRC, "rq_host.cpp"), blob,
+        os.path.join(CSRC, "rq_host.cpp"), os.path.join(CSRC, "rq_gguf.cpp"), blob,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
         "-o", tmp,
     ])

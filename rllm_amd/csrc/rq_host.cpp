@@ -12,14 +12,18 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
+#include "rq_internal.h"
 #include "rq_params.h"
 
 extern "C" const unsigned char rq_kernels_blob[];  // rq_kernels.hip: Q8_1 pass, dot4 matvecs
@@ -93,7 +97,11 @@ int block_bytes(int type) {
 const char* const kFmtSuffix[RQ_NUM_FMTS] = {"q4_0", "q8_0", "q4_k", "q6_k"};
 
 constexpr size_t kPlaneAlign = 256;
-constexpr size_t kUploadChunkBytes = size_t(64) << 20;  // as UPLOAD_CHUNK_BYTES, backend.rs:110
+// Upload staging: GGUF bytes go host -> pinned buffer (parallel memcpy) ->
+// device staging (DMA) -> repack kernel, in chunks of about this size, two
+// chunks in flight (the reference stages up to UPLOAD_CHUNK_BYTES = 64 MiB
+// through pageable copies, backend.rs:110, 1326-1361).
+constexpr size_t kUploadChunkBytes = size_t(16) << 20;
 // LDS a 256-thread matvec workgroup may stage activations in (two such
 // workgroups share a CU's LDS). The 1024-thread workgroups, one per CU, may
 // use what the device allows a workgroup (rq_ctx::lds_wide).
@@ -103,9 +111,87 @@ constexpr int kLdsPerSb = 400;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Host threads that split a memcpy (the copy into pinned memory runs at a
+// few GB/s per thread; the DMA behind it at PCIe speed). The caller takes
+// the first share; workers take the rest and report completion.
+class CopyPool {
+  public:
+    explicit CopyPool(int workers) {
+        for (int i = 0; i < workers; i++) threads_.emplace_back([this, i] { run(i); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : threads_) t.join();
+    }
+    void copy(void* dst, const void* src, size_t n) {
+        const size_t parts = threads_.size() + 1;
+        if (n < (size_t(1) << 20) || parts == 1) {
+            memcpy(dst, src, n);
+            return;
+        }
+        const size_t share = align_up((n + parts - 1) / parts, 4096);
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            dst_ = (uint8_t*)dst;
+            src_ = (const uint8_t*)src;
+            n_ = n;
+            share_ = share;
+            pending_ = (int)threads_.size();
+            gen_++;
+        }
+        cv_.notify_all();
+        memcpy(dst, src, std::min(share, n));
+        std::unique_lock<std::mutex> g(mu_);
+        done_.wait(g, [this] { return pending_ == 0; });
+    }
+
+  private:
+    void run(int i) {
+        uint64_t seen = 0;
+        for (;;) {
+            uint8_t* dst;
+            const uint8_t* src;
+            size_t lo, hi;
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+                dst = dst_;
+                src = src_;
+                lo = std::min(n_, share_ * (size_t)(i + 1));
+                hi = std::min(n_, share_ * (size_t)(i + 2));
+            }
+            if (hi > lo) memcpy(dst + lo, src + lo, hi - lo);
+            {
+                std::lock_guard<std::mutex> g(mu_);
+                if (--pending_ == 0) done_.notify_one();
+            }
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    uint8_t* dst_ = nullptr;
+    const uint8_t* src_ = nullptr;
+    size_t n_ = 0, share_ = 0;
+    int pending_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 }  // namespace
+
+rq_status rq_fail_msg(rq_status code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
 
 struct rq_ctx {
     int device = 0;
@@ -146,6 +232,14 @@ struct rq_ctx {
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
     hipStream_t stream = nullptr;
+    // Upload staging (created by the first rq_upload, kept until rq_close):
+    // two pinned host buffers, two device buffers and the events that mark
+    // each pinned buffer's DMA done.
+    size_t up_cap = 0;
+    void* up_pin[2] = {};
+    void* up_dev[2] = {};
+    hipEvent_t up_ev[2] = {};
+    CopyPool* up_pool = nullptr;
 };
 
 struct rq_weight {
@@ -617,6 +711,11 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     if (!ctx) return fail(RQ_ERR_BACKEND, "rq_open: out of host memory");
     ctx->device = device;
     auto bail = [&](rq_status st) {
+        for (int b = 0; b < 2; b++) {
+            if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
+            if (ctx->up_dev[b]) (void)hipFree(ctx->up_dev[b]);
+            if (ctx->up_ev[b]) (void)hipEventDestroy(ctx->up_ev[b]);
+        }
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
         if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
         delete ctx;
@@ -731,6 +830,7 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
         if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
     }
+    delete ctx->up_pool;
     delete ctx;
     return st;
 }
@@ -745,6 +845,33 @@ extern "C" rq_status rq_device_info(rq_ctx* ctx, int* compute_units, char* arch_
     if (!ctx) return fail(RQ_ERR_INVALID, "rq_device_info: null context");
     if (compute_units) *compute_units = ctx->cus;
     if (arch_name && arch_len) snprintf(arch_name, arch_len, "%s", ctx->arch);
+    return RQ_OK;
+}
+
+// The context's upload staging, grown to `bytes` per buffer on demand.
+static rq_status upload_staging(rq_ctx* ctx, size_t bytes) {
+    if (!ctx->up_pool) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        const int workers = (int)std::min<unsigned>(7, hw > 2 ? hw / 2 - 1 : 0);
+        ctx->up_pool = new (std::nothrow) CopyPool(workers);
+        if (!ctx->up_pool) return fail(RQ_ERR_BACKEND, "rq_upload: out of host memory");
+    }
+    for (int b = 0; b < 2; b++) {
+        if (!ctx->up_ev[b]) HIP_TRY(hipEventCreateWithFlags(&ctx->up_ev[b], hipEventDisableTiming));
+    }
+    if (ctx->up_cap >= bytes) return RQ_OK;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (int b = 0; b < 2; b++) {
+        if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
+        if (ctx->up_dev[b]) (void)hipFree(ctx->up_dev[b]);
+        ctx->up_pin[b] = ctx->up_dev[b] = nullptr;
+    }
+    ctx->up_cap = 0;
+    for (int b = 0; b < 2; b++) {
+        HIP_TRY(hipHostMalloc(&ctx->up_pin[b], bytes, hipHostMallocDefault));
+        HIP_TRY(hipMalloc(&ctx->up_dev[b], bytes));
+    }
+    ctx->up_cap = bytes;
     return RQ_OK;
 }
 
@@ -808,25 +935,35 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
     e = hipMemsetAsync(w->base, 0, total, ctx->stream);
 
     const int64_t chunk_rows = std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)(kUploadChunkBytes / rb)));
-    void* staging = nullptr;
-    if (e == hipSuccess) e = hipMalloc(&staging, (size_t)(chunk_rows * rb));
-    if (e != hipSuccess) {
+    if (e == hipSuccess) st = upload_staging(ctx, (size_t)(chunk_rows * rb));
+    if (e != hipSuccess || st != RQ_OK) {
+        if (e != hipSuccess) st = hip_fail("hipMemsetAsync", e);
         (void)hipFree(w->base);
         delete w;
-        return hip_fail("hipMalloc", e);
+        return st;
     }
-    for (int64_t row0 = 0; row0 < rows && st == RQ_OK; row0 += chunk_rows) {
+    // Two chunks in flight: while the DMA engine copies chunk i out of one
+    // pinned buffer (and the repack kernel follows it on the stream), the
+    // host threads fill the other with chunk i + 1.
+    for (int64_t row0 = 0, i = 0; row0 < rows && st == RQ_OK; row0 += chunk_rows, i++) {
+        const int b = (int)(i & 1);
         const int64_t n = std::min(chunk_rows, rows - row0);
-        e = hipMemcpyAsync(staging, (const uint8_t*)gguf + row0 * rb, (size_t)(n * rb), hipMemcpyHostToDevice,
-                           ctx->stream);
+        if (i >= 2 && (e = hipEventSynchronize(ctx->up_ev[b])) != hipSuccess) {
+            st = hip_fail("hipEventSynchronize", e);
+            break;
+        }
+        ctx->up_pool->copy(ctx->up_pin[b], (const uint8_t*)gguf + row0 * rb, (size_t)(n * rb));
+        e = hipMemcpyAsync(ctx->up_dev[b], ctx->up_pin[b], (size_t)(n * rb), hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(ctx->up_ev[b], ctx->stream);
         if (e != hipSuccess) {
             st = hip_fail("hipMemcpyAsync", e);
             break;
         }
+        const uint8_t* staging = (const uint8_t*)ctx->up_dev[b];
         if (w->mmq) {
             RqMmqRepackParams p;
             memset(&p, 0, sizeof p);
-            p.raw = (const uint8_t*)staging;
+            p.raw = staging;
             p.code = (uint8_t*)w->code;
             p.hdr = (uint8_t*)w->hdr;
             p.row0 = row0;
@@ -838,7 +975,7 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
         } else {
             RqRepackParams p;
             memset(&p, 0, sizeof p);
-            p.raw = (const uint8_t*)staging;
+            p.raw = staging;
             p.main = (uint8_t*)w->tiled.main;
             p.tail = (uint8_t*)w->tiled.tail;
             p.row0 = row0;
@@ -849,10 +986,9 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
             st = launch(ctx, ctx->repack[fmt], "rq_repack", (uint64_t)((n * p.S + RQ_THREADS - 1) / RQ_THREADS), &p);
         }
     }
-    // Keep `staging` alive until the repack kernels have read it.
+    // The staging buffers are reused by the next upload: wait for this one.
     e = hipStreamSynchronize(ctx->stream);
     if (st == RQ_OK && e != hipSuccess) st = hip_fail("hipStreamSynchronize", e);
-    (void)hipFree(staging);
     if (st != RQ_OK) {
         (void)hipFree(w->base);
         delete w;

@@ -1,0 +1,52 @@
+"""GGUF file -> device weight (rq_gguf_upload) on the GPU: the same weight as
+rq_upload of the same bytes (exact GGUF round trip, identical matvec
+outputs), for every quantized type and both kernel families."""
+import numpy as np
+import pytest
+
+import gguf_writer as W
+from gpu_util import upload
+from rllm_amd.errors import GgufError, ShapeError, UnsupportedError
+from rllm_amd.gguf import GgufFile
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"q4_k": (12, 96, 1024), "q6_k": (14, 48, 512), "q8_0": (8, 80, 256), "q4_0": (2, 32, 512)}
+
+
+def _file(tmp_path, orc):
+    tensors = [(f"blk.0.{n}.weight", [k, r], t, orc.random_weight(5 + t, t, r, k).tobytes())
+               for n, (t, r, k) in SHAPES.items()]
+    tensors += [("blk.0.attn_norm.weight", [256], 0, np.ones(256, np.float32).tobytes()),
+                ("blk.0.f32_2d", [32, 4], 0, np.ones(128, np.float32).tobytes())]
+    buf, _ = W.model_file([("general.architecture", W.STRING, "llama")], tensors, alignment=64)
+    p = tmp_path / "model.gguf"
+    p.write_bytes(buf)
+    return str(p), tensors
+
+
+def test_upload_from_gguf(gpuk, orc, tmp_path):
+    path, tensors = _file(tmp_path, orc)
+    with GgufFile(path) as g:
+        for name, (t, r, k) in [(f"blk.0.{n}.weight", v) for n, v in SHAPES.items()]:
+            raw = g.tensor_data(g.require_tensor(name))
+            wg = gpuk.upload_gguf(g, name)
+            assert np.array_equal(gpuk.weight_to_gguf(wg), raw), name
+            wb = upload(gpuk, t, np.array(raw), r, k)
+            x = gpuk.from_host(orc.normal(9, 3 * k))
+            a, b = gpuk.alloc(3 * r), gpuk.alloc(3 * r)
+            gpuk.matmul(x, wg, a, 3)
+            gpuk.matmul(x, wb, b, 3)
+            # bit patterns (random blocks can carry NaN / Inf scales)
+            assert np.array_equal(gpuk.to_host(a, 3 * r).view(np.uint32), gpuk.to_host(b, 3 * r).view(np.uint32)), name
+
+
+def test_upload_from_gguf_errors(gpu, orc, tmp_path):
+    path, _ = _file(tmp_path, orc)
+    with GgufFile(path) as g:
+        with pytest.raises(GgufError, match="missing tensor nope"):
+            gpu.upload_gguf(g, "nope")
+        with pytest.raises(ShapeError, match="1-d tensor"):
+            gpu.upload_gguf(g, "blk.0.attn_norm.weight")
+        with pytest.raises(UnsupportedError, match="GGML type 0"):
+            gpu.upload_gguf(g, "blk.0.f32_2d")
