@@ -26,6 +26,27 @@ __device__ __forceinline__ u16 f2h_mul(float a, float b) {
     return f2h(p);
 }
 
+// A wave-uniform value the compiler must treat as produced right here. The
+// kernels pick their launch target by value from fields at static kernarg
+// offsets; passing each candidate through this keeps the pick a value select
+// (s_cselect) after one batch of scalar loads, where the compiler would
+// otherwise load from a selected address, a load that waits for the
+// selector and delays every address computed from the target.
+template <class V>
+__device__ __forceinline__ V sgpr_value(V v) {
+    __asm__ volatile("" : "+s"(v));
+    return v;
+}
+
+// Global-memory access through a pointer the compiler cannot trace to a
+// kernel argument (after sgpr_value): without the address space it would use
+// flat instructions, which also count against lgkmcnt, so every LDS wait
+// would wait for them too.
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gmem(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
@@ -50,11 +71,12 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 // v_dot4_i32_i8: c + sum of the four signed byte products.
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Streaming 16-byte load: weights are read once, so the nontemporal hint
-// keeps them from displacing reusable lines (activations) in the caches.
+// Streaming 16-byte load of global memory: weights are read once, so the
+// nontemporal hint keeps them from displacing reusable lines (activations) in
+// the caches.
 __device__ __forceinline__ int4 ld16_nt(const u8* p) {
     typedef int v4i_nt __attribute__((ext_vector_type(4)));
-    const v4i_nt v = __builtin_nontemporal_load((const v4i_nt*)p);
+    const v4i_nt v = __builtin_nontemporal_load((const __attribute__((address_space(1))) v4i_nt*)p);
     return make_int4(v.x, v.y, v.z, v.w);
 }
 

@@ -113,7 +113,7 @@ __device__ __forceinline__ void load_sb(const RqTiled& w, int t, int a, SB<FMT>&
     const u8* base = w.main + ((int64_t)t * C * slots + a) * 16;
 #pragma unroll
     for (int c = 0; c < C; c++) o.c[c] = ld16_nt(base + (int64_t)c * slots * 16);
-    o.tail = FMT == RQ_FMT_Q6_K ? (u32) * (const u16*)(w.tail + ((int64_t)t * slots + a) * 2) : 0u;
+    o.tail = FMT == RQ_FMT_Q6_K ? (u32) * gmem((const u16*)(w.tail + ((int64_t)t * slots + a) * 2)) : 0u;
 }
 
 // One 32-value activation block (sub-block j of a super-block) of one column.
@@ -307,7 +307,7 @@ __device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? w.
 __device__ __forceinline__ void tile_store(const RqMvTarget& T, int t, int lane, int rt, int g, float v, int col) {
     v = group_sum(v, g);
     const int row = t * T.w.R + rt;
-    if (group_leader(lane, g) && rt < T.w.R && row < T.n) T.out[(int64_t)col * T.n + row] = v;
+    if (group_leader(lane, g) && rt < T.w.R && row < T.n) gmem(T.out)[(int64_t)col * T.n + row] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -356,15 +356,17 @@ struct StageItem {
     bool store, valid;
 };
 
+// Staging item it: block it % (8 S) of column it / (8 S) (one column: no
+// division).
+template <int NC>
 __device__ __forceinline__ StageItem stage_item(int it, int total, int S, int U) {
     StageItem si;
     si.store = it < total;
     const int itc = si.store ? it : total - 1;
-    si.col = itc / (8 * S);
-    const int rem = itc % (8 * S);
-    si.s = rem >> 3;
-    si.j = rem & 7;
-    si.b = 8 * si.s + si.j;
+    si.col = NC == 1 ? 0 : itc / (8 * S);
+    si.b = NC == 1 ? itc : itc - si.col * (8 * S);
+    si.s = si.b >> 3;
+    si.j = si.b & 7;
     si.valid = si.b < U;
     return si;
 }
@@ -399,7 +401,7 @@ struct QItem {
 
 __device__ __forceinline__ void qitem_load(const float* __restrict__ xf, int k, int total, int S, int U, int base,
                                            QItem& q) {
-    q.si = stage_item(base + (threadIdx.x >> 2), total, S, U);
+    q.si = stage_item<1>(base + (threadIdx.x >> 2), total, S, U);
     const float4* p = (const float4*)(xf + (int64_t)q.si.col * k + (int64_t)(q.si.valid ? q.si.b : 0) * 32 +
                                       8 * (threadIdx.x & 3));
     const float4 a = p[0], b = p[1];
@@ -490,8 +492,8 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
             qitem_write<FMT>(q, S);
         }
     } else {
-        StageItem si0 = stage_item(threadIdx.x, total, S, U);
-        StageItem si1 = stage_item(threadIdx.x + THREADS, total, S, U);
+        StageItem si0 = stage_item<NC>(threadIdx.x, total, S, U);
+        StageItem si1 = stage_item<NC>(threadIdx.x + THREADS, total, S, U);
         XJ x0, x1;
         load_x_raw(xq + (int64_t)si0.col * k, xd + (int64_t)si0.col * U, si0.valid ? si0.b : 0, x0);
         load_x_raw(xq + (int64_t)si1.col * k, xd + (int64_t)si1.col * U, si1.valid ? si1.b : 0, x1);
@@ -500,13 +502,34 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
         stage_write<FMT>(si0, x0, S);
         stage_write<FMT>(si1, x1, S);
         for (int it = threadIdx.x + 2 * THREADS; it < total; it += THREADS) {
-            const StageItem si = stage_item(it, total, S, U);
+            const StageItem si = stage_item<NC>(it, total, S, U);
             XJ x;
             load_x_raw(xq + (int64_t)si.col * k, xd + (int64_t)si.col * U, si.valid ? si.b : 0, x);
             stage_write<FMT>(si, x, S);
         }
     }
     __syncthreads();
+}
+
+// Target ti of a launch (see sgpr_value).
+__device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
+    RqMvTarget r;
+#define RQ_PICK(f)                                                                                        \
+    {                                                                                                     \
+        const auto a = sgpr_value(P.t[0].f), b = sgpr_value(P.t[1].f), c = sgpr_value(P.t[2].f);          \
+        r.f = ti == 0 ? a : (ti == 1 ? b : c);                                                            \
+    }
+    RQ_PICK(w.main)
+    RQ_PICK(w.tail)
+    RQ_PICK(w.S)
+    RQ_PICK(w.R)
+    RQ_PICK(w.T)
+    RQ_PICK(w.k)
+    RQ_PICK(out)
+    RQ_PICK(n)
+    RQ_PICK(wave_start)
+#undef RQ_PICK
+    return r;
 }
 
 template <int FMT, int NC, bool F32IN, int WAVES>
@@ -518,9 +541,9 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     int ti = 0;
     if (P.count > 1 && gwave >= P.t[1].wave_start) ti = 1;
     if (P.count > 2 && gwave >= P.t[2].wave_start) ti = 2;
-    // By value, selected from fields at static kernarg offsets (a reference
-    // indexed by ti reloads its fields with dependent scalar loads at each use).
-    const RqMvTarget T = ti == 0 ? P.t[0] : (ti == 1 ? P.t[1] : P.t[2]);
+    // By value (a reference indexed by ti reloads its fields with dependent
+    // scalar loads at each use).
+    const RqMvTarget T = pick_target(P, ti);
     const int t = gwave - T.wave_start;  // this wave's tile
     const bool has_tile = t < T.w.T;     // wave-uniform
     const int R = T.w.R, slots = R * S;

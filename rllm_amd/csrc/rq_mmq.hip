@@ -235,6 +235,25 @@ __device__ __forceinline__ Scales<FMT, MP> scales_of(const int4 h, bool hsel, in
     return r;
 }
 
+// Target ti of a launch, by value (see sgpr_value).
+__device__ __forceinline__ RqMmqTarget pick_target(const RqMmqParams& P, int ti) {
+    RqMmqTarget r;
+#define RQ_PICK(f)                                                                                        \
+    {                                                                                                     \
+        const auto a = sgpr_value(P.t[0].f), b = sgpr_value(P.t[1].f), c = sgpr_value(P.t[2].f);          \
+        r.f = ti == 0 ? a : (ti == 1 ? b : c);                                                            \
+    }
+    RQ_PICK(code)
+    RQ_PICK(hdr)
+    RQ_PICK(out)
+    RQ_PICK(n)
+    RQ_PICK(tiles)
+    RQ_PICK(wg_start)
+#undef RQ_PICK
+    r.pad = 0;
+    return r;
+}
+
 // ---------------------------------------------------------------------------
 // The matvec (and, with DOTS, the block-dot debug kernel).
 
@@ -262,10 +281,9 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     int ti = 0;
     if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
     if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
-    // By value, selected from fields at static kernarg offsets: a reference
-    // indexed by ti would reload its fields (dependent scalar loads) at every
-    // use, including in the final reduction.
-    const RqMmqTarget T = ti == 0 ? P.t[0] : (ti == 1 ? P.t[1] : P.t[2]);
+    // By value: a reference indexed by ti would reload its fields (dependent
+    // scalar loads) at every use, including in the final reduction.
+    const RqMmqTarget T = pick_target(P, ti);
     const int ks = P.ks;
     const int tl = wave / ks, kpart = wave - (wave / ks) * ks;
     const int tile = (blk - T.wg_start) * P.tr + tl;
@@ -404,7 +422,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                     int dot = D[v];
                     if (FMT == RQ_FMT_Q4_K) dot = hi ? (dot >> 4) + 8 * sq : dot;
                     if (FMT == RQ_FMT_Q4_0) dot = hi ? (dot >> 4) : dot - 8 * sq;
-                    if (a < P.m && row < T.n && b < U) dots[((int64_t)a * T.n + row) * U + b] = dot;
+                    if (a < P.m && row < T.n && b < U) gmem(dots)[((int64_t)a * T.n + row) * U + b] = dot;
                 }
                 continue;
             }
@@ -511,7 +529,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                 s += part[(w * 64 + 16 * (a >> 1) + nn) * 2 + (a & 1)];
             }
         }
-        out[(int64_t)ag * T.n + row] = s;
+        gmem(out)[(int64_t)ag * T.n + row] = s;
     }
 }
 
