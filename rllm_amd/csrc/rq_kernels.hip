@@ -302,12 +302,37 @@ __device__ __forceinline__ float sb_value(const SB<FMT>& w, const XJ* x) {
 // Lane group size of a tile's row: S lanes when R > 1 (S a power of two), else the wave.
 __device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? w.S : 64; }
 
-// Reduce the lane's partial for tile t and store its row's result
-// (rt = the lane's row within the tile; R means none).
-__device__ __forceinline__ void tile_store(const RqMvTarget& T, int t, int lane, int rt, int g, float v, int col) {
-    v = group_sum(v, g);
-    const int row = t * T.w.R + rt;
-    if (group_leader(lane, g) && rt < T.w.R && row < T.n) gmem(T.out)[(int64_t)col * T.n + row] = v;
+// The lane's row within a tile (R: none). Tiles of R > 1 rows have S a power
+// of two (R * S = 64), so this is a shift, not a division.
+__device__ __forceinline__ int tile_row(const RqTiled& w, int lane) {
+    if (lane >= w.R * w.S) return w.R;
+    return w.R > 1 ? lane >> (31 - __builtin_clz(w.S)) : 0;
+}
+
+// The super-block column of slot a (a < R * S).
+__device__ __forceinline__ int tile_col(const RqTiled& w, int a) { return w.R > 1 ? a & (w.S - 1) : a; }
+
+// Where a lane's row sum goes: worked out before the weights arrive, so the
+// tail of the wave is the reduction and one store.
+struct RowDst {
+    float* out;  // the row's column-0 result
+    int g;       // lanes per row group
+    bool store;  // this lane is its group's leader for a real row
+};
+
+__device__ __forceinline__ RowDst row_dst(const RqMvTarget& T, int t, int lane) {
+    const int rt = tile_row(T.w, lane), row = t * T.w.R + rt;
+    RowDst d;
+    d.g = row_group(T.w);
+    d.store = group_leader(lane, d.g) && rt < T.w.R && row < T.n;
+    d.out = T.out + (d.store ? row : 0);
+    return d;
+}
+
+// Reduce the lane's partial and store its row's result for column col.
+__device__ __forceinline__ void tile_store(const RowDst& d, int64_t n, float v, int col) {
+    v = group_sum(v, d.g);
+    if (d.store) gmem(d.out)[(int64_t)col * n] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -548,6 +573,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     const bool has_tile = t < T.w.T;     // wave-uniform
     const int R = T.w.R, slots = R * S;
     const int a0 = lane < slots ? lane : 0;
+    const RowDst dst = row_dst(T, t, lane);
 
     // The tile's weight loads (clamped to a valid tile; waves without one
     // discard it) go out right behind round 0 of the staging loads.
@@ -559,7 +585,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = 0.f;
-    slot_dot<FMT, NC>(w, S, a0 % S, lane < slots, acc);
+    slot_dot<FMT, NC>(w, S, tile_col(T.w, a0), lane < slots, acc);
     // Rows wider than 64 super-blocks: further slot passes (R = 1).
     for (int a = lane + 64; a - lane < slots; a += 64) {
         const bool active = a < slots;
@@ -567,10 +593,8 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
         load_sb<FMT>(T.w, t, active ? a : 0, w2);
         slot_dot<FMT, NC>(w2, S, active ? a : 0, active, acc);
     }
-    const int rt = lane < slots ? lane / S : R;
-    const int g = row_group(T.w);
 #pragma unroll
-    for (int c = 0; c < NC; c++) tile_store(T, t, lane, rt, g, acc[c], c);
+    for (int c = 0; c < NC; c++) tile_store(dst, T.n, acc[c], c);
 }
 
 #define RQ_MVX(NAME, FMT, NC)                                                                                         \
@@ -669,14 +693,14 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
         float acc[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) acc[c] = 0.f;
-        slot_dot<FMT, NC>(w, S, a0 % S, lane < slots, acc);
+        slot_dot<FMT, NC>(w, S, tile_col(P.gate, a0), lane < slots, acc);
         for (int a = lane + 64; a - lane < slots; a += 64) {  // rows wider than 64 super-blocks
             const bool active = a < slots;
             SB<FMT> w2;
             load_sb<FMT>(tile_w(q), tile_t(q), active ? a : 0, w2);
             slot_dot<FMT, NC>(w2, S, active ? a : 0, active, acc);
         }
-        const int rt = lane < slots ? lane / S : R;
+        const int rt = tile_row(P.gate, lane);
         const int g = R > 1 ? S : 64;
         const int row = (q < NT ? q : q - NT) * R + rt;  // row within the block
 #pragma unroll
