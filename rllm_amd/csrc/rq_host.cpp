@@ -466,7 +466,7 @@ int mmq_sbw_index(int sbw) { return sbw == 2 ? 0 : sbw == 4 ? 1 : 2; }
 // Most super-blocks per wave the format's kernels exist for (Q8_0 keeps 16 B
 // of codes per window in registers, so it stops at 4).
 int mmq_sbw_max(int fmt) { return fmt == RQ_FMT_Q8_0 ? 4 : 8; }
-int mmq_planes(int fmt) { return fmt == RQ_FMT_Q4_K ? 3 : fmt == RQ_FMT_Q4_0 ? 2 : 1; }
+int mmq_planes(int fmt) { return fmt == RQ_FMT_Q8_0 ? 1 : 2; }
 int mmq_S2(int64_t cols) { return (int)((cols + 511) / 512 * 2); }
 
 // A workgroup holds the ks <= 16 waves of a tile's k-parts.

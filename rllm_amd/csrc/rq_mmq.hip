@@ -42,7 +42,7 @@ struct MF;
 template <>
 struct MF<RQ_FMT_Q4_K> {
     static constexpr bool NIB = true;
-    static constexpr int NPL = 3;  // planes: dxe, f, f8
+    static constexpr int NPL = 2;  // planes: dxe, f8
 };
 template <>
 struct MF<RQ_FMT_Q4_0> {
@@ -68,11 +68,12 @@ __device__ __forceinline__ float half_f(u32 w, int i) { return h2f(i ? (w >> 16)
 // Activation staging. Per (column a, 32-element block b): the codes at
 // a * kxp + 32 b, and per-block planes of floats, plane p at
 // pl_off + ((p * MP + a) * NB + b) * 4 (NB = 8 * S2 blocks per padded row):
-//   Q4_K  dxe = dx (dx / 16 in high windows), f = dx * sum q, f8 = 8 f in high windows (else 0)
-//   Q4_0  dxe as Q4_K, fo = -8 f in low windows (else 0)
+//   Q4_K  dxe = dx (dx / 16 in high windows), f8 = 8 dx sum q
+//   Q4_0  dxe as Q4_K, fo = -8 dx sum q in low windows (else 0)
 //   Q8_0  dx
 // where dx is the f32 value of the block's f16 scale. A block is in a high
-// window when (b / 2) is odd. The dots kernels add an int plane of sum q.
+// window when (b / 2) is odd, which every lane's entries know at compile
+// time. The dots kernels add an int plane of sum q.
 // Blocks past k and columns past m are staged as zeros.
 
 template <int FMT, int MP, bool DOTS>
@@ -83,10 +84,8 @@ __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b,
     char* pl = mmq_lds + P.pl_off + (a * NB + b) * 4;
     const bool hi = (b >> 1) & 1;
     if (FMT == RQ_FMT_Q4_K) {
-        const float f = dx * (float)sq;
         *(float*)pl = hi ? dx * 0.0625f : dx;
-        *(float*)(pl + stride) = f;
-        *(float*)(pl + 2 * stride) = hi ? 8.f * f : 0.f;
+        *(float*)(pl + stride) = 8.f * (dx * (float)sq);
     } else if (FMT == RQ_FMT_Q4_0) {
         const float f = dx * (float)sq;
         *(float*)pl = hi ? dx * 0.0625f : dx;
@@ -368,6 +367,12 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
         for (int wp = 0; wp < NPH; wp++) A[wp] = v4i{0, 0, 0, 0};
 
         const int stride = MP * NB * 4;  // bytes between planes
+        // The lane's plane addresses at this k-part's first block (each
+        // D-group then reads at compile-time offsets from them): mp <= 4 one
+        // activation, mp = 8 two (2 g, 2 g + 1).
+        const int a_lane = MP == 1 ? 0 : MP == 2 ? (g >> 1) : MP == 4 ? g : 2 * g;
+        const int lb_lane = MP == 1 ? 4 * g : MP == 2 ? 4 * (g & 1) : 0;
+        const char* plb = mmq_lds + P.pl_off + (a_lane * NB + sb0 * 8 + lb_lane) * 4;
 #pragma unroll
         for (int t = 0; t < ND; t++) {
             if (t * NPH * 64 >= nsb * 256) break;  // a short last k-part (uniform)
@@ -427,26 +432,29 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                 continue;
             }
 
+            // The lane's entries are blocks of one window half: high (stored
+            // XOR 8, scaled by 16) when the block's window is odd, known here
+            // at compile time: (lb0 + v) / 2 is odd exactly when v / 2 (mp <=
+            // 4) or t (mp = 8) is.
             if (MP <= 4) {
-                const int a = MP == 1 ? 0 : MP == 2 ? (g >> 1) : g;
-                const int pofs = P.pl_off + (a * NB + pb) * 4;
-                const float4 p0 = *(const float4*)(mmq_lds + pofs);
+                const int lbo = MP == 1 ? 16 * t : MP == 2 ? 8 * t : 4 * t;  // lb0 - lb_lane
+                const float4 p0 = *(const float4*)(plb + 4 * lbo);
                 const float pv0[4] = {p0.x, p0.y, p0.z, p0.w};
                 if (FMT == RQ_FMT_Q4_K) {
-                    const float4 p1 = *(const float4*)(mmq_lds + pofs + stride);
-                    const float4 p2 = *(const float4*)(mmq_lds + pofs + 2 * stride);
-                    const float pv1[4] = {p1.x, p1.y, p1.z, p1.w}, pv2[4] = {p2.x, p2.y, p2.z, p2.w};
+                    const float4 p1 = *(const float4*)(plb + 4 * lbo + stride);
+                    const float pv1[4] = {p1.x, p1.y, p1.z, p1.w};
                     float accd = 0.f, accm = 0.f;
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        const float tv = fmaf(pv0[v], (float)D[v], pv2[v]);
+                        const bool hiw = (v >> 1) & 1;
+                        const float tv = hiw ? fmaf(pv0[v], (float)D[v], pv1[v]) : pv0[v] * (float)D[v];
                         accd = fmaf(byte_f(sc.sc, v), tv, accd);
                         accm = fmaf(byte_f(sc.mn, v), pv1[v], accm);
                     }
                     y[gi][0] = fmaf(sc.d, accd, y[gi][0]);
-                    y[gi][0] = fmaf(-sc.dmin, accm, y[gi][0]);
+                    y[gi][0] = fmaf(-0.125f * sc.dmin, accm, y[gi][0]);
                 } else if (FMT == RQ_FMT_Q4_0) {
-                    const float4 p1 = *(const float4*)(mmq_lds + pofs + stride);
+                    const float4 p1 = *(const float4*)(plb + 4 * lbo + stride);
                     const float pv1[4] = {p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
@@ -459,28 +467,27 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                         y[gi][0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), pv0[v] * (float)D[v], y[gi][0]);
                 }
             } else {  // mp = 8: two activations per lane, blocks pb, pb + 1
+                const bool hiw = t & 1;
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    const int a = 2 * g + e;
-                    const int pofs = P.pl_off + (a * NB + pb) * 4;
-                    const float2 p0 = *(const float2*)(mmq_lds + pofs);
+                    const char* pe = plb + e * NB * 4 + 8 * t;
+                    const float2 p0 = *(const float2*)pe;
                     const float pv0[2] = {p0.x, p0.y};
                     if (FMT == RQ_FMT_Q4_K) {
-                        const float2 p1 = *(const float2*)(mmq_lds + pofs + stride);
-                        const float2 p2 = *(const float2*)(mmq_lds + pofs + 2 * stride);
-                        const float pv1[2] = {p1.x, p1.y}, pv2[2] = {p2.x, p2.y};
+                        const float2 p1 = *(const float2*)(pe + stride);
+                        const float pv1[2] = {p1.x, p1.y};
                         const int bsh = jb & 3;  // byte of block jb in its scale word
                         float accd = 0.f, accm = 0.f;
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
-                            const float tv = fmaf(pv0[h], (float)D[2 * e + h], pv2[h]);
+                            const float tv = hiw ? fmaf(pv0[h], (float)D[2 * e + h], pv1[h]) : pv0[h] * (float)D[2 * e + h];
                             accd = fmaf(byte_f(sc.sc, bsh + h), tv, accd);
                             accm = fmaf(byte_f(sc.mn, bsh + h), pv1[h], accm);
                         }
                         y[gi][e] = fmaf(sc.d, accd, y[gi][e]);
-                        y[gi][e] = fmaf(-sc.dmin, accm, y[gi][e]);
+                        y[gi][e] = fmaf(-0.125f * sc.dmin, accm, y[gi][e]);
                     } else if (FMT == RQ_FMT_Q4_0) {
-                        const float2 p1 = *(const float2*)(mmq_lds + pofs + stride);
+                        const float2 p1 = *(const float2*)(pe + stride);
                         const float pv1[2] = {p1.x, p1.y};
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
