@@ -215,6 +215,8 @@ struct rq_ctx {
     hipFunction_t gluf[RQ_NUM_FMTS] = {};                   // the same from one f32 column
     hipFunction_t act_mul = nullptr;
     hipFunction_t norm[4] = {};  // rq_rms_norm_<vpt>, vpt = 1, 2, 4, 8
+    hipFunction_t mvxm[2][RQ_MV_MAX_NC + 1] = {};  // Q4_K + Q6_K targets in one launch
+    hipFunction_t mvfm[2] = {};
     // Q8_1 of the gated FFN's product h (rq_gated_ffn), grown like sq/sd/ss.
     int8_t* hq = nullptr;
     uint16_t* hd = nullptr;
@@ -319,6 +321,8 @@ bool mv_wide(int R, int64_t m, bool f32_in) { return R < 4 && (f32_in || m >= 2)
 rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
                         const rq_weight* const* ws, float* const* outs, int count) {
     const int fmt = ws[0]->fmt;
+    bool mixed = false;
+    for (int i = 1; i < count; i++) mixed |= ws[i]->fmt != fmt;
     const int64_t k = ws[0]->cols, U = (k + 31) / 32;
     const int S = ws[0]->tiled.S;
     const int wide = mv_wide(ws[0]->tiled.R, m, xf != nullptr) ? 1 : 0;
@@ -348,12 +352,23 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
         p.count = count;
         p.m = nc;
         const uint64_t blocks = (uint64_t)((waves + waves_per_wg - 1) / waves_per_wg);
-        rq_status st = launch(ctx, xf ? ctx->mvf[wide][fmt] : ctx->mvx[wide][fmt][nc], xf ? "rq_mvf" : "rq_mvx",
-                              blocks, &p, (unsigned)(nc * kLdsPerSb * S), (unsigned)(64 * waves_per_wg));
+        hipFunction_t f = mixed ? (xf ? ctx->mvfm[wide] : ctx->mvxm[wide][nc])
+                                : (xf ? ctx->mvf[wide][fmt] : ctx->mvx[wide][fmt][nc]);
+        rq_status st = launch(ctx, f, xf ? "rq_mvf" : "rq_mvx", blocks, &p, (unsigned)(nc * kLdsPerSb * S),
+                              (unsigned)(64 * waves_per_wg));
         if (st != RQ_OK) return st;
         g0 += nc;
     }
     return RQ_OK;
+}
+
+// Whether weights a and b can share one matvec launch: the same type and
+// kernel family, or Q4_K and Q6_K in the dot4 layout (the mixed kernels).
+bool launch_compatible(const rq_weight* a, const rq_weight* b) {
+    if (a->mmq != b->mmq) return false;
+    if (a->type == b->type) return true;
+    const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
+    return !a->mmq && ka && kb;
 }
 
 // Grows a Q8_1 scratch (codes q, scales d and s, capacity cap) to `values`
@@ -750,6 +765,15 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
         snprintf(nname, sizeof nname, "rq_rms_norm_%d", 1 << i);
         st = get(&ctx->norm[i], nname);
     }
+    for (int wide = 0; wide < 2 && st == RQ_OK; wide++) {
+        char nname[48];
+        for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {
+            snprintf(nname, sizeof nname, "rq_mvxm%s_q4_k_q6_k_%d", wide ? "w" : "", nc);
+            st = get(&ctx->mvxm[wide][nc], nname);
+        }
+        snprintf(nname, sizeof nname, "rq_mvfm%s_q4_k_q6_k", wide ? "w" : "");
+        if (st == RQ_OK) st = get(&ctx->mvfm[wide], nname);
+    }
     char name[64];
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
         for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {
@@ -913,6 +937,7 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
         total = align_up(align_up(w->code_bytes, kPlaneAlign) + w->hdr_bytes, kPlaneAlign);
     } else {
         tile_geometry(rows, cols, w->tiled);
+        w->tiled.fmt = fmt;
         const int64_t slots = (int64_t)w->tiled.T * w->tiled.R * w->tiled.S;
         w->main_bytes = (size_t)(slots * rq_chunks(fmt) * 16);
         w->tail_bytes = fmt == RQ_FMT_Q6_K ? (size_t)(slots * 2) : 0;
@@ -1125,11 +1150,11 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
     for (int i = 0; i < count; i++) {
         if (!ws[i] || !outs[i]) return fail(RQ_ERR_INVALID, "matvec: null weight or output %d", i);
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matvec: output %d not 4-byte aligned", i);
-        if (ws[i]->type != ws[0]->type)
-            return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
-                        type_name(ws[i]->type));
         if (ws[i]->mmq != ws[0]->mmq)
             return fail(RQ_ERR_SHAPE, "matvec: weights laid out for different kernel families in one launch");
+        if (!launch_compatible(ws[0], ws[i]))
+            return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
+                        type_name(ws[i]->type));
         if (ws[i]->cols != ws[0]->cols)
             return fail(RQ_ERR_SHAPE, "matmul_many: mixed input widths %lld and %lld", (long long)ws[0]->cols,
                         (long long)ws[i]->cols);
@@ -1199,8 +1224,12 @@ extern "C" rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, 
     int i = 0;
     while (i < count) {
         int g = 1;
-        while (g < RQ_MV_TARGETS && i + g < count && ws[i + g]->type == ws[i]->type && ws[i + g]->mmq == ws[i]->mmq)
+        while (g < RQ_MV_TARGETS && i + g < count) {
+            bool ok = true;
+            for (int j = i; j < i + g; j++) ok = ok && launch_compatible(ws[j], ws[i + g]);
+            if (!ok) break;
             g++;
+        }
         if (ws[i]->mmq)
             st = fused ? mmq_launch(ctx, nullptr, nullptr, x, m, ws + i, (void* const*)(outs + i), g, false)
                        : mmq_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, (void* const*)(outs + i), g, false);

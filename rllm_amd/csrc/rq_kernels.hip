@@ -10,6 +10,7 @@
 //   rq_mvx_<fmt>_<nc>    matvec over nc = 1..8 Q8_1 activation columns (staged in LDS)
 //   rq_mvf_<fmt>         one f32 activation column, quantized while staging
 //   rq_mvxw_*, rq_mvfw_* the same with 1024-thread (Q8_0: 512) workgroups (tiles of < 4 rows)
+//   rq_mvxm_q4_k_q6_k_<nc>, rq_mvfm_q4_k_q6_k (+ w) launches mixing Q4_K and Q6_K targets
 //   rq_glu_<fmt>_<nc>    gated FFN front half act(gate . x) * (up . x) + its Q8_1 (rq_gluf_*: f32 x)
 //   rq_act_mul           elementwise act(g) * u, optionally with Q8_1 of the result
 //   rq_rms_norm_<vpt>    RMS norm of rows (optionally after x += y), optionally with Q8_1
@@ -156,8 +157,8 @@ __device__ __forceinline__ void prep_x(XJ& x, bool valid) {
             sb = dot4(x.q[4 + i], 0x01010101, sb);
         }
         if (FMT == RQ_FMT_Q4_0) x.ia = -8 * (sa + sb);
-        if (FMT == RQ_FMT_Q4_K) x.f = x.dx * (float)(sa + sb);
-        if (FMT == RQ_FMT_Q6_K) {
+        if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K) x.f = x.dx * (float)(sa + sb);
+        if (FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K) {
             x.ia = -32 * sa;
             x.ib = -32 * sb;
         }
@@ -463,9 +464,10 @@ __device__ __forceinline__ void qitem_write(QItem& q, int S) {
             const int sa = pair, sb = other;
             XMeta m;
             m.dx = h2f(f2h(d));
-            m.f = FMT == RQ_FMT_Q4_K ? m.dx * (float)(sa + sb) : 0.f;
-            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * (sa + sb) : (FMT == RQ_FMT_Q6_K ? -32 * sa : 0);
-            m.ib = FMT == RQ_FMT_Q6_K ? -32 * sb : 0;
+            const bool k4 = FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K, k6 = FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K;
+            m.f = k4 ? m.dx * (float)(sa + sb) : 0.f;
+            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * (sa + sb) : (k6 ? -32 * sa : 0);
+            m.ib = k6 ? -32 * sb : 0;
             *(XMeta*)(rec + 256 + 16 * q.si.j) = m;
         }
     }
@@ -550,10 +552,12 @@ __device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
     RQ_PICK(w.R)
     RQ_PICK(w.T)
     RQ_PICK(w.k)
+    RQ_PICK(w.fmt)
     RQ_PICK(out)
     RQ_PICK(n)
     RQ_PICK(wave_start)
 #undef RQ_PICK
+    r.w.pad = 0;
     return r;
 }
 
@@ -613,6 +617,88 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvfw_##NAME(RqMvParams p) {              \
         mvx_body<FMT, 1, true, RQ_MV_WIDE_THREADS(FMT) / 64>(p);                                                      \
     }
+
+// Launches whose targets mix Q4_K and Q6_K weights of one width (q, k and v
+// of a Q4_K_M layer in one launch). The staged records carry both formats'
+// sums, each wave runs its own target's format, and the weights land in one
+// register block sized for Q6_K (Q4_K fills the first 9 chunks), so the two
+// formats share registers instead of adding up.
+template <int NC, bool F32IN, int WAVES>
+__device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
+    const int lane = threadIdx.x & 63;
+    const int gwave = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int S = P.t[0].w.S, k = P.t[0].w.k;
+    int ti = 0;
+    if (P.count > 1 && gwave >= P.t[1].wave_start) ti = 1;
+    if (P.count > 2 && gwave >= P.t[2].wave_start) ti = 2;
+    const RqMvTarget T = pick_target(P, ti);
+    const bool q6 = T.w.fmt == RQ_FMT_Q6_K;  // wave-uniform
+    const int t = gwave - T.wave_start;
+    const bool has_tile = t < T.w.T;
+    const int R = T.w.R, slots = R * S;
+    const int a0 = lane < slots ? lane : 0;
+    const RowDst dst = row_dst(T, t, lane);
+
+    SB<RQ_FMT_Q6_K> w;  // Q4_K: chunks 0..8
+    auto load = [&](int tt, int a) {
+        if (q6) {
+            load_sb<RQ_FMT_Q6_K>(T.w, tt, a, w);
+        } else {
+            SB<RQ_FMT_Q4_K> w4;
+            load_sb<RQ_FMT_Q4_K>(T.w, tt, a, w4);
+#pragma unroll
+            for (int c = 0; c < Fmt<RQ_FMT_Q4_K>::C; c++) w.c[c] = w4.c[c];
+        }
+    };
+    auto dot = [&](int a, bool active, float* acc) {
+        if (q6) {
+            slot_dot<RQ_FMT_Q6_K, NC>(w, S, a, active, acc);
+        } else {
+            SB<RQ_FMT_Q4_K> w4;
+#pragma unroll
+            for (int c = 0; c < Fmt<RQ_FMT_Q4_K>::C; c++) w4.c[c] = w.c[c];
+            w4.tail = 0u;
+            slot_dot<RQ_FMT_Q4_K, NC>(w4, S, a, active, acc);
+        }
+    };
+    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] { load(has_tile ? t : T.w.T - 1, a0); });
+    if (!has_tile) return;
+
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) acc[c] = 0.f;
+    dot(tile_col(T.w, a0), lane < slots, acc);
+    for (int a = lane + 64; a - lane < slots; a += 64) {  // rows wider than 64 super-blocks (R = 1)
+        const bool active = a < slots;
+        load(t, active ? a : 0);
+        dot(active ? a : 0, active, acc);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) tile_store(dst, T.n, acc[c], c);
+}
+
+#define RQ_MVXM(NC)                                                                                                   \
+    extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvxm_q4_k_q6_k_##NC(RqMvParams p) {                   \
+        mvx_mix_body<NC, false, RQ_WAVES>(p);                                                                         \
+    }                                                                                                                 \
+    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K)) void rq_mvxmw_q4_k_q6_k_##NC(            \
+        RqMvParams p) {                                                                                               \
+        mvx_mix_body<NC, false, RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K) / 64>(p);                                             \
+    }
+RQ_MVXM(1)
+RQ_MVXM(2)
+RQ_MVXM(3)
+RQ_MVXM(4)
+RQ_MVXM(5)
+RQ_MVXM(6)
+RQ_MVXM(7)
+RQ_MVXM(8)
+extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvfm_q4_k_q6_k(RqMvParams p) {
+    mvx_mix_body<1, true, RQ_WAVES>(p);
+}
+extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K)) void rq_mvfmw_q4_k_q6_k(RqMvParams p) {
+    mvx_mix_body<1, true, RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K) / 64>(p);
+}
 
 #define RQ_MVX_ALL(NAME, FMT) \
     RQ_MVX(NAME, FMT, 1)      \

@@ -38,6 +38,9 @@
 #define RQ_FMT_Q4_K 2
 #define RQ_FMT_Q6_K 3
 #define RQ_NUM_FMTS 4
+// Staging pseudo-format of launches that mix Q4_K and Q6_K targets (Q4_K_M
+// files keep attn_v and ffn_down in Q6_K): records carry both formats' sums.
+#define RQ_FMT_MIX_K 8
 
 // Chunks of 16 bytes per super-block, by format.
 static inline int rq_chunks(int fmt) { return fmt == RQ_FMT_Q8_0 ? 17 : (fmt == RQ_FMT_Q6_K ? 13 : 9); }
@@ -64,6 +67,8 @@ struct RqTiled {
     int32_t R;            // rows per tile
     int32_t T;            // tiles
     int32_t k;            // columns
+    int32_t fmt;          // RQ_FMT_* (chosen per wave in mixed launches)
+    int32_t pad;
 };
 
 struct RqMvTarget {

@@ -174,7 +174,7 @@ def test_matmul_operator(gpuk, orc, m):
 
 @pytest.mark.parametrize("m", [1, 2])
 def test_matmul_many_grouping(gpuk, orc, m):
-    """Backend::matmul_many over a mixed list: runs of <= 3 same-type weights share a launch."""
+    """Backend::matmul_many over a mixed list: runs of <= 3 weights of one type (or Q4_K and Q6_K, dot4) share a launch."""
     k = 1024
     spec = [(12, 64), (12, 32), (14, 48), (12, 16), (12, 96), (12, 8), (12, 40), (8, 24), (2, 56)]
     ws, wgs, outs = [], [], []
@@ -190,6 +190,31 @@ def test_matmul_many_grouping(gpuk, orc, m):
         orc.assert_close(f"many type {t} rows {n}", orc.matvec_q8_1(t, w, n, k, qs, d, m), gpuk.to_host(o, m * n), TOL_B)
 
 
+@pytest.mark.parametrize("k", [1024, 4096, 14336, 20480])
+@pytest.mark.parametrize("m", [1, 3])
+def test_mixed_q4k_q6k_launch(gpu, orc, k, m):
+    """q, k (Q4_K) and v (Q6_K) of a Q4_K_M layer share one launch (rq_mvxm /
+    rq_mvfm): each output is bit-identical to its own single-weight launch."""
+    spec = [(12, 64), (12, 16), (14, 16)] if k <= 4096 else [(12, 12), (14, 5), (12, 7)]
+    ws = [make_weight(orc, t, n, k, 700 + i, "random") for i, (t, n) in enumerate(spec)]
+    wgs = [upload(gpu, t, w, n, k) for (t, n), w in zip(spec, ws)]
+    x = gpu.from_host(_x(orc, 701, m, k))
+    together = [gpu.alloc(m * n) for _, n in spec]
+    gpu.matmul_many(x, wgs, together, m)
+    xq = gpu.quantize_q8_1(x, m, k)
+    via_q8 = [gpu.alloc(m * n) for _, n in spec]
+    gpu.matvec_many(xq, wgs, via_q8, m)
+    for (t, n), wg, a, b in zip(spec, wgs, together, via_q8):
+        alone = gpu.alloc(m * n)
+        gpu.matmul(x, wg, alone, m)
+        want = gpu.to_host(alone, m * n).view(np.uint32)
+        assert np.array_equal(gpu.to_host(a, m * n).view(np.uint32), want), f"type {t} rows {n} (matmul_many)"
+        alone_q = gpu.alloc(m * n)
+        gpu.matvec(xq, wg, alone_q, m)
+        assert np.array_equal(gpu.to_host(b, m * n).view(np.uint32),
+                              gpu.to_host(alone_q, m * n).view(np.uint32)), f"type {t} rows {n} (matvec_many)"
+
+
 @pytest.mark.parametrize("tname", list(TYPES))
 def test_upload_roundtrip(gpuk, orc, tname):
     """The repack moves bytes only: downloading it back gives the GGUF bytes."""
@@ -202,7 +227,7 @@ def test_upload_roundtrip(gpuk, orc, tname):
 
 
 def test_upload_chunked(gpuk, orc):
-    """Q6_K 30000 x 4096 is 100.8 MB of GGUF bytes: two 64 MiB staging chunks."""
+    """Q6_K 30000 x 4096 is 100.8 MB of GGUF bytes: seven ~16 MiB staging chunks through two pinned buffers."""
     t, n, k = 14, 30000, 4096
     w = make_weight(orc, t, n, k, 2024, "random")
     wg = upload(gpuk, t, w, n, k)
