@@ -226,9 +226,9 @@ struct rq_ctx {
     // 2, 4, 8) and super-blocks per wave (sbw = 2, 4, 8); null where a
     // format has none.
     hipModule_t mmq_mod = nullptr;
-    hipFunction_t mmq[RQ_NUM_FMTS][4][3] = {};
+    hipFunction_t mmq[RQ_NUM_FMTS][3][3] = {};
     hipFunction_t mmqf[RQ_NUM_FMTS][3] = {};
-    hipFunction_t mmqd[RQ_NUM_FMTS][4][3] = {};
+    hipFunction_t mmqd[RQ_NUM_FMTS][3][3] = {};
     hipFunction_t mmqg[RQ_NUM_FMTS][2][3] = {};  // 8 x G columns, G = 2, 4
     hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
@@ -473,10 +473,10 @@ rq_status act_mul_launch(rq_ctx* ctx, int act, float* g, const float* u, int64_t
 // ---------------------------------------------------------------------------
 // int8-MFMA kernels over 16-row tiles (rq_mmq.hip, layout in rq_params.h).
 
-constexpr int kMmqMp[4] = {1, 2, 4, 8};
+constexpr int kMmqMp[3] = {1, 4, 8};
 constexpr int kMmqSbw[3] = {2, 4, 8};
 
-int mmq_mp_index(int mp) { return mp == 1 ? 0 : mp == 2 ? 1 : mp == 4 ? 2 : 3; }
+int mmq_mp_index(int mp) { return mp == 1 ? 0 : mp == 4 ? 1 : 2; }
 int mmq_sbw_index(int sbw) { return sbw == 2 ? 0 : sbw == 4 ? 1 : 2; }
 // Most super-blocks per wave the format's kernels exist for (Q8_0 keeps 16 B
 // of codes per window in registers, so it stops at 4).
@@ -491,7 +491,7 @@ bool mmq_supported(int fmt, int64_t cols) {
     return (mmq_S2(cols) + maxs - 1) / maxs <= 16;
 }
 
-// Columns per launch: up to 8 in one staged group (mp = 1, 2, 4, 8), or 8 x g
+// Columns per launch: up to 8 in one staged group (mp = 1, 4, 8), or 8 x g
 // (g = 2, 4) staged one group after another against weights read once.
 constexpr int kMmqMaxCols = 32;
 
@@ -585,9 +585,11 @@ int pow2_at_least(int v) {
 }
 
 // Column grouping of an MFMA launch of nc columns: mp (columns staged at
-// once) and g (groups of 8 staged in turn).
+// once: 1, 4 or 8) and g (groups of 8 staged in turn). Two columns run in
+// the 4-column class, whose shorter D-groups beat a 2-column class (Q4_K
+// 14336 x 4096: 8.40 against 9.76 us).
 void mmq_cols(int nc, int& mp, int& g) {
-    mp = nc <= 8 ? pow2_at_least(nc) : 8;
+    mp = nc <= 1 ? 1 : nc <= 4 ? 4 : 8;
     g = nc <= 8 ? 1 : (nc <= 16 ? 2 : 4);
 }
 
@@ -810,7 +812,7 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
                 snprintf(name, sizeof name, "rq_mmq_%s_8x%d_%d", kFmtSuffix[f], gi == 0 ? 2 : 4, kMmqSbw[si]);
                 st = getm(ctx->mmq_mod, &ctx->mmqg[f][gi][si], name);
             }
-            for (int mi = 0; mi < 4 && st == RQ_OK; mi++) {
+            for (int mi = 0; mi < 3 && st == RQ_OK; mi++) {
                 snprintf(name, sizeof name, "rq_mmq_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
                 if ((st = getm(ctx->mmq_mod, &ctx->mmq[f][mi][si], name)) != RQ_OK) break;
                 snprintf(name, sizeof name, "rq_mmqd_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);

@@ -1,7 +1,7 @@
 // gfx950 int8-MFMA matvec kernels of librq.so, over the 16-row tile weight
 // layout documented in rq_params.h.
 //
-//   rq_mmq_<fmt>_<mp>_<sbw>  Q8_1 activations, up to mp = 1, 2, 4, 8 columns
+//   rq_mmq_<fmt>_<mp>_<sbw>  Q8_1 activations, up to mp = 1, 4, 8 columns
 //   rq_mmq_<fmt>_8x<g>_<sbw> up to 8 g columns (g = 2, 4 groups of 8, weights read once)
 //   rq_mmqf_<fmt>_<sbw>      one f32 activation column, quantized while staging
 //   rq_mmqd_<fmt>_<mp>_<sbw> the int32 block dots of the same MFMA path (debug)
@@ -553,7 +553,6 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     }
 #define RQ_MMQ_SET(NAME, FMT, SBW)                                                               \
     RQ_MMQ(NAME, FMT, 1, SBW)                                                                    \
-    RQ_MMQ(NAME, FMT, 2, SBW)                                                                    \
     RQ_MMQ(NAME, FMT, 4, SBW)                                                                    \
     RQ_MMQ(NAME, FMT, 8, SBW)                                                                    \
     RQ_MMQ_G(NAME, FMT, 2, SBW)                                                                  \

@@ -88,3 +88,49 @@ def test_capture_without_reserve_is_an_error(orc):
     finally:
         fresh.synchronize()
         fresh.close()
+
+
+def test_layer_graph_replays(gpu, orc):
+    """One Q4_K_M-style layer as a graph: add_rms_norm with its Q8_1 copy
+    feeding q/k/v in one mixed Q4_K/Q6_K launch (rq_matvec_many), rms_norm
+    + gated_ffn; every replay bit-identical to eager calls on the same
+    inputs (the norm's in-place residual update included)."""
+    from rllm_amd.backend import Activation, Q8_1
+
+    d, f = 1024, 2048
+    q = upload(gpu, 12, make_weight(orc, 12, d, d, 81, "normal"), d, d)
+    kk = upload(gpu, 12, make_weight(orc, 12, 256, d, 82, "normal"), 256, d)
+    v = upload(gpu, 14, make_weight(orc, 14, 256, d, 83, "normal"), 256, d)
+    gate = upload(gpu, 12, make_weight(orc, 12, f, d, 84, "normal"), f, d)
+    up = upload(gpu, 12, make_weight(orc, 12, f, d, 85, "normal"), f, d)
+    down = upload(gpu, 14, make_weight(orc, 14, d, f, 86, "normal"), d, f)
+    nw = gpu.from_host(orc.normal(87, d, 1.0, 0.1))
+    gpu.reserve(f)
+    x, y = gpu.alloc(d), gpu.alloc(d)
+    normed, hq = gpu.alloc(d), Q8_1.empty(d, gpu.device)
+    outs = [gpu.alloc(d), gpu.alloc(256), gpu.alloc(256)]
+    ffn_out, gb, ub = gpu.alloc(d), gpu.alloc(f), gpu.alloc(f)
+
+    def step(o, fo):
+        gpu.add_rms_norm(x, y, nw, normed, 1, d, 1e-6, hq)
+        gpu.matvec_many(hq, [q, kk, v], o, 1)
+        gpu.rms_norm(x, nw, normed, 1, 1e-6)
+        gpu.gated_ffn(normed, gate, up, down, Activation.SILU, fo, gb, ub, 1)
+
+    g = _capture(gpu, lambda: step(outs, ffn_out))
+    for rep in range(4):
+        x0, y0 = orc.normal(30 + rep, d), orc.normal(40 + rep, d)
+        x.copy_(torch.from_numpy(x0).to(gpu.device))
+        y.copy_(torch.from_numpy(y0).to(gpu.device))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [gpu.to_host(o).copy() for o in outs] + [gpu.to_host(ffn_out).copy(), gpu.to_host(x).copy()]
+        x.copy_(torch.from_numpy(x0).to(gpu.device))
+        y.copy_(torch.from_numpy(y0).to(gpu.device))
+        e_outs, e_ffn = [gpu.alloc(d), gpu.alloc(256), gpu.alloc(256)], gpu.alloc(d)
+        step(e_outs, e_ffn)
+        torch.cuda.synchronize()
+        want = [gpu.to_host(o).copy() for o in e_outs] + [gpu.to_host(e_ffn).copy(), gpu.to_host(x).copy()]
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep} output {i}"
