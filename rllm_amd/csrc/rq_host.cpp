@@ -296,7 +296,11 @@ rq_status check_q8_1(const char* what, const rq_q8_1* xq, int64_t values) {
 void tile_geometry(int64_t rows, int64_t cols, RqTiled& t) {
     t.k = (int32_t)cols;
     t.S = (int32_t)((cols + 255) / 256);
-    t.R = (t.S <= 32 && is_pow2(t.S)) ? 64 / t.S : 1;
+    // Rows of S <= 32 super-blocks get aligned groups of S rounded up to a
+    // power of two lanes (64 / R each); wider rows take the whole wave.
+    int sp = 1;
+    while (sp < t.S) sp *= 2;
+    t.R = t.S <= 32 ? 64 / sp : 1;
     t.T = (int32_t)((rows + t.R - 1) / t.R);
 }
 

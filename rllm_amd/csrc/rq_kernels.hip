@@ -300,18 +300,40 @@ __device__ __forceinline__ float sb_value(const SB<FMT>& w, const XJ* x) {
 // ---------------------------------------------------------------------------
 // Row reduction and store.
 
-// Lane group size of a tile's row: S lanes when R > 1 (S a power of two), else the wave.
-__device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? w.S : 64; }
+// Lanes of a tile. Tiles of R > 1 rows (S <= 32 super-blocks per row) give
+// each row an aligned group of Sp = 64 / R lanes (S rounded up to a power of
+// two): lane l is super-block l % Sp of row l / Sp, a real one when
+// l % Sp < S. Tiles are stored densely (R rows of S slots), so lane l reads
+// slot (l / Sp) * S + l % Sp; a padding lane reads its row's first slot again
+// (the same address as a real lane of the same load: no extra traffic) and
+// contributes nothing. R == 1 (S > 32): lane l is super-block l, then l + 64,
+// ... (several passes when S > 64).
+struct TileLane {
+    int row;    // row within the tile (its group's row for padding lanes)
+    int col;    // super-block column of the lane's slot
+    int slot;   // storage slot the lane reads
+    bool real;  // a slot of the row, not padding
+};
 
-// The lane's row within a tile (R: none). Tiles of R > 1 rows have S a power
-// of two (R * S = 64), so this is a shift, not a division.
-__device__ __forceinline__ int tile_row(const RqTiled& w, int lane) {
-    if (lane >= w.R * w.S) return w.R;
-    return w.R > 1 ? lane >> (31 - __builtin_clz(w.S)) : 0;
+__device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane) {
+    TileLane r;
+    if (w.R > 1) {
+        const int sh = __builtin_ctz(64 / w.R);  // log2(Sp)
+        r.row = lane >> sh;
+        r.col = lane & ((1 << sh) - 1);
+        r.real = r.col < w.S;
+        if (!r.real) r.col = 0;
+    } else {
+        r.row = 0;
+        r.real = lane < w.S;
+        r.col = r.real ? lane : 0;
+    }
+    r.slot = r.row * w.S + r.col;
+    return r;
 }
 
-// The super-block column of slot a (a < R * S).
-__device__ __forceinline__ int tile_col(const RqTiled& w, int a) { return w.R > 1 ? a & (w.S - 1) : a; }
+// Lanes per row group: Sp when R > 1, else the wave.
+__device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? 64 / w.R : 64; }
 
 // Where a lane's row sum goes: worked out before the weights arrive, so the
 // tail of the wave is the reduction and one store.
@@ -322,7 +344,7 @@ struct RowDst {
 };
 
 __device__ __forceinline__ RowDst row_dst(const RqMvTarget& T, int t, int lane) {
-    const int rt = tile_row(T.w, lane), row = t * T.w.R + rt;
+    const int rt = tile_lane(T.w, lane).row, row = t * T.w.R + rt;
     RowDst d;
     d.g = row_group(T.w);
     d.store = group_leader(lane, d.g) && rt < T.w.R && row < T.n;
@@ -575,21 +597,21 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     const RqMvTarget T = pick_target(P, ti);
     const int t = gwave - T.wave_start;  // this wave's tile
     const bool has_tile = t < T.w.T;     // wave-uniform
-    const int R = T.w.R, slots = R * S;
-    const int a0 = lane < slots ? lane : 0;
+    const int slots = T.w.R * S;  // stored slots per tile
+    const TileLane tl = tile_lane(T.w, lane);
     const RowDst dst = row_dst(T, t, lane);
 
     // The tile's weight loads (clamped to a valid tile; waves without one
     // discard it) go out right behind round 0 of the staging loads.
     SB<FMT> w;
     stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
-                                         [&] { load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, a0, w); });
+                                         [&] { load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, tl.slot, w); });
     if (!has_tile) return;  // wave-uniform; no barrier follows
 
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = 0.f;
-    slot_dot<FMT, NC>(w, S, tile_col(T.w, a0), lane < slots, acc);
+    slot_dot<FMT, NC>(w, S, tl.col, tl.real, acc);
     // Rows wider than 64 super-blocks: further slot passes (R = 1).
     for (int a = lane + 64; a - lane < slots; a += 64) {
         const bool active = a < slots;
@@ -635,8 +657,8 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const bool q6 = T.w.fmt == RQ_FMT_Q6_K;  // wave-uniform
     const int t = gwave - T.wave_start;
     const bool has_tile = t < T.w.T;
-    const int R = T.w.R, slots = R * S;
-    const int a0 = lane < slots ? lane : 0;
+    const int slots = T.w.R * S;
+    const TileLane tl = tile_lane(T.w, lane);
     const RowDst dst = row_dst(T, t, lane);
 
     SB<RQ_FMT_Q6_K> w;  // Q4_K: chunks 0..8
@@ -661,13 +683,14 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
             slot_dot<RQ_FMT_Q4_K, NC>(w4, S, a, active, acc);
         }
     };
-    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] { load(has_tile ? t : T.w.T - 1, a0); });
+    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
+                                                  [&] { load(has_tile ? t : T.w.T - 1, tl.slot); });
     if (!has_tile) return;
 
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = 0.f;
-    dot(tile_col(T.w, a0), lane < slots, acc);
+    dot(tl.col, tl.real, acc);
     for (int a = lane + 64; a - lane < slots; a += 64) {  // rows wider than 64 super-blocks (R = 1)
         const bool active = a < slots;
         load(t, active ? a : 0);
@@ -761,7 +784,8 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
     const int S = P.gate.S, R = P.gate.R, k = P.gate.k;
     const int NT = 32 / R;  // tiles of each weight in the 32-row block
     const int blk = blockIdx.x;
-    const int slots = R * S, a0 = lane < slots ? lane : 0;
+    const int slots = R * S;
+    const TileLane tl = tile_lane(P.gate, lane);
     // Tile q of the block (q < NT: gate, else up), row tile index of its weight.
     auto tile_w = [&](int q) -> const RqTiled& { return q < NT ? P.gate : P.up; };
     auto tile_t = [&](int q) { return blk * NT + (q < NT ? q : q - NT); };
@@ -769,25 +793,25 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
 
     SB<FMT> w;
     stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
-                                         [&] { load_sb<FMT>(tile_w(q0), tile_t(q0), a0, w); });
+                                         [&] { load_sb<FMT>(tile_w(q0), tile_t(q0), tl.slot, w); });
     // g and u of the block, per column: floats after the staged records.
     float* gu = (float*)(rq_lds + NC * S * RQ_LDS_REC);
     for (int q = wave; q < 2 * NT; q += WAVES) {  // uniform per wave
         // Next tile's loads go out before this tile's arithmetic.
         SB<FMT> wn;
-        if (q + WAVES < 2 * NT) load_sb<FMT>(tile_w(q + WAVES), tile_t(q + WAVES), a0, wn);
+        if (q + WAVES < 2 * NT) load_sb<FMT>(tile_w(q + WAVES), tile_t(q + WAVES), tl.slot, wn);
         float acc[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++) acc[c] = 0.f;
-        slot_dot<FMT, NC>(w, S, tile_col(P.gate, a0), lane < slots, acc);
+        slot_dot<FMT, NC>(w, S, tl.col, tl.real, acc);
         for (int a = lane + 64; a - lane < slots; a += 64) {  // rows wider than 64 super-blocks
             const bool active = a < slots;
             SB<FMT> w2;
             load_sb<FMT>(tile_w(q), tile_t(q), active ? a : 0, w2);
             slot_dot<FMT, NC>(w2, S, active ? a : 0, active, acc);
         }
-        const int rt = tile_row(P.gate, lane);
-        const int g = R > 1 ? S : 64;
+        const int rt = tl.row;
+        const int g = row_group(P.gate);
         const int row = (q < NT ? q : q - NT) * R + rt;  // row within the block
 #pragma unroll
         for (int c = 0; c < NC; c++) {

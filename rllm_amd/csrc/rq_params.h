@@ -6,10 +6,11 @@
 // super-blocks of 256 consecutive elements of a row (Q8_0 and Q4_0: eight
 // GGUF blocks; a row's last super-block may be partial, its missing blocks
 // stored as zeros). A row has S = ceil(k / 256) super-blocks. A tile is R
-// rows x S super-blocks, R = 64 / S when S is a power of two <= 32 and 1
-// otherwise; tile t holds rows [R t, R t + R) (rows past n are zeros). In a
-// tile, super-block s of row r occupies slot a = (r - R t) * S + s, and one
-// wave lane serves one slot. Each super-block is cut into C chunks of 16
+// rows x S super-blocks, R = 64 / Sp with Sp = S rounded up to a power of
+// two when S <= 32, and 1 otherwise; tile t holds rows [R t, R t + R) (rows
+// past n are zeros). In a tile, super-block s of row r occupies slot
+// a = (r - R t) * S + s (stored densely), and the wave lane r Sp + s serves
+// it (lanes with s >= S are padding). Each super-block is cut into C chunks of 16
 // bytes; the main plane stores chunk c of every slot of tile t contiguously,
 //     main + ((t * C + c) * R * S + a) * 16,
 // so each of a wave's chunk loads is one contiguous run of 16 B per lane.

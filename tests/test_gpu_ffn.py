@@ -65,6 +65,20 @@ def test_glu_matmul(gpuk, orc, tname, m, act):
     orc.assert_close(f"glu {tname} {act.name} m={m}", want, gpuk.to_host(out, m * n), 1e-3)
 
 
+@pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("k", [1792, 5120])
+@pytest.mark.parametrize("m", [1, 2])
+def test_glu_matmul_odd_width(gpuk, orc, tname, k, m):
+    """Rows of S = 7 and 20 super-blocks (tiles of 8 and 2 rows, padded lane groups)."""
+    t, n = TYPES[tname], 64
+    gw, uw, g, u, x = _glu_case(gpuk, orc, t, n, k, m, 60 + k + m, "random")
+    out, us = gpuk.alloc(m * n), gpuk.alloc(m * n)
+    gpuk.glu_matmul(gpuk.from_host(x), g, u, Activation.SILU, out, us, m)
+    qs, d, _ = orc.quantize_q8_1(x, m, k)
+    want = orc.glu_q8_1(t, gw, uw, n, k, qs, d, m, int(Activation.SILU))
+    orc.assert_close(f"glu {tname} k={k} m={m}", want, gpuk.to_host(out, m * n), 1e-3)
+
+
 @pytest.mark.parametrize("tname", ["Q8_0", "Q4_K", "Q6_K"])
 @pytest.mark.parametrize("m", [1, 3, 70])
 @pytest.mark.parametrize("act", ACTS)

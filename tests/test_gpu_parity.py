@@ -128,6 +128,30 @@ def test_matvec_all_types(gpuk, orc, tname, m):
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("k", [768, 1792, 5120, 7168])
+@pytest.mark.parametrize("m", [1, 3])
+def test_odd_widths(gpuk, orc, tname, k, m):
+    """Rows of S = 3, 7, 20, 28 super-blocks: tiles of R = 16, 8, 2, 2 rows in
+    padded lane groups (dot4); block dots bit-exact, f32 within the bars,
+    through rq_matvec (Q8_1) and rq_matmul (f32, quantized in the launch)."""
+    t = TYPES[tname]
+    n = 67
+    w = make_weight(orc, t, n, k, 17 * k + m, "random")
+    wg = upload(gpuk, t, w, n, k)
+    x = _x(orc, 3 + k, m, k)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    xq = q8_1_to_device(gpuk, qs, d, s)
+    assert np.array_equal(gpuk.block_dots(xq, wg, m).cpu().numpy(), orc.block_dots(t, w, n, k, qs, m))
+    want = orc.matvec_q8_1(t, w, n, k, qs, d, m)
+    out = gpuk.alloc(m * n)
+    gpuk.matvec(xq, wg, out, m)
+    orc.assert_close(f"{tname} k={k} matvec", want, gpuk.to_host(out, m * n), TOL_B)
+    out2 = gpuk.alloc(m * n)
+    gpuk.matmul(gpuk.from_host(x), wg, out2, m)
+    orc.assert_close(f"{tname} k={k} matmul", want, gpuk.to_host(out2, m * n), TOL_B)
+
+
+@pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("n,k", [(1, 256), (5, 256), (130, 2048), (257, 4096), (40, 14336)])
 def test_matvec_shapes(gpuk, orc, tname, n, k):
     t = TYPES[tname]
