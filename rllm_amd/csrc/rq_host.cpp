@@ -116,8 +116,15 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // the first share; workers take the rest and report completion.
 class CopyPool {
   public:
+    // Up to `workers` threads: fewer if the system refuses more.
     explicit CopyPool(int workers) {
-        for (int i = 0; i < workers; i++) threads_.emplace_back([this, i] { run(i); });
+        for (int i = 0; i < workers; i++) {
+            try {
+                threads_.emplace_back([this, i] { run(i); });
+            } catch (...) {
+                break;
+            }
+        }
     }
     ~CopyPool() {
         {
@@ -183,8 +190,6 @@ class CopyPool {
     uint64_t gen_ = 0;
     bool stop_ = false;
 };
-
-bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 }  // namespace
 
@@ -582,11 +587,6 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int g, int64_t tile
     return best;
 }
 
-int pow2_at_least(int v) {
-    int p = 1;
-    while (p < v) p *= 2;
-    return p;
-}
 
 // Column grouping of an MFMA launch of nc columns: mp (columns staged at
 // once: 1, 4 or 8) and g (groups of 8 staged in turn). Two columns run in
