@@ -135,6 +135,32 @@ def bench_matvec(torch, gpu, orc, t, n, k, m, steps, warmup, seed=7, family=None
             "bytes": b, "kernels": family}
 
 
+def bench_cold(torch, gpu, orc, t, n, k, reps=7, seed=7):
+    """One eager launch after 1 GiB of writes has flushed L2 and the
+    Infinity Cache (weights and activations come from HBM, the launch is not
+    in a graph): the median over `reps` of HIP-event time on the stream."""
+    from rllm_amd.backend import HostTensor
+    from rllm_amd.dtype import DType
+
+    w = gpu.upload(HostTensor("cold", DType(t), (n, k), make_gguf(orc, t, n, k, seed)))
+    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(seed + 1, k)), 1, k)
+    out = gpu.alloc(n)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=gpu.device)
+    times = []
+    for i in range(reps):
+        flush.fill_(i & 0xFF)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(gpu.stream)
+        gpu.matvec(xq, w, out, 1)
+        e1.record(gpu.stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1000.0)
+    del flush
+    w.free()
+    times.sort()
+    return times[len(times) // 2]
+
+
 def bench_decode(torch, gpu, orc, replays):
     """tok/s of the 8B-shape decode step's linear layers, as one HIP graph."""
     from rllm_amd.backend import HostTensor
@@ -322,6 +348,9 @@ def main() -> int:
     log(f"Q4_K {N}x{K} m=1 ({r['kernels']}): {r['us']:.2f} us/launch, {r['gbs']:.0f} GB/s "
         f"({100 * r['gbs'] / HBM_PEAK_GBS:.1f}% of peak), {r['copies']} copies, check rel {r['check_rel']:.1e}")
 
+    cold_us = bench_cold(torch, gpu, orc, T, N, K)
+    log(f"cold (caches flushed, one eager launch): {cold_us:.2f} us, {alg_bytes(T, N, K, 1) / cold_us / 1e3:.0f} GB/s")
+
     configs = []
     if args.all_configs:
         # BASELINE configs 1-4 in the default family; config 5 (small batch,
@@ -330,6 +359,10 @@ def main() -> int:
                 ("Q8_0", 8, 11008, 4096, 1, None), ("Q6_K", 14, 4096, 14336, 1, None),
                 ("Q6_K", 14, 128256, 4096, 1, None)]
         plan += [("Q4_K", 12, 14336, 4096, m, fam) for m in (1, 2, 4, 8, 16, 32) for fam in ("dot4", "mfma")]
+        # One GPU's share at tensor-parallel degree 8 (row slices of gate and
+        # the head, a k slice of down): the kernels at their real shard shapes.
+        plan += [("Q4_K shard", 12, 1792, 4096, 1, None), ("Q6_K shard", 14, 4096, 1792, 1, None),
+                 ("Q6_K shard", 14, 16032, 4096, 1, None)]
         for name, t, n, k, m, fam in plan:
             c = bench_matvec(torch, gpu, orc, t, n, k, m, max(256, args.steps // 4), 256, family=fam)
             log(f"config {name} {n}x{k} m={m} ({c['kernels']}): {c['us']:.2f} us, {c['gbs']:.0f} GB/s "
@@ -363,6 +396,7 @@ def main() -> int:
                    "rows": N, "cols": K, "batch": 1, "weight_copies": r["copies"],
                    "timing": "HIP graph replay, HIP events"},
         "pct_hbm_peak": round(100 * r["gbs"] / HBM_PEAK_GBS, 2),
+        "cold_us": round(cold_us, 2),
         "decode_tok_s": round(dec["tok_s"], 1) if dec else None,
         "decode_step_us": round(dec["us"], 1) if dec else None,
         "upload_gbs": round(dec["upload_gbs"], 1) if dec else None,
