@@ -359,6 +359,8 @@ def main() -> int:
                 ("Q8_0", 8, 11008, 4096, 1, None), ("Q6_K", 14, 4096, 14336, 1, None),
                 ("Q6_K", 14, 128256, 4096, 1, None)]
         plan += [("Q4_K", 12, 14336, 4096, m, fam) for m in (1, 2, 4, 8, 16, 32) for fam in ("dot4", "mfma")]
+        # The same small batches over a Q6_K weight (ffn_down of a Q4_K_M file).
+        plan += [("Q6_K", 14, 4096, 14336, m, fam) for m in (4, 8, 16, 32) for fam in ("dot4", "mfma")]
         # One GPU's share at tensor-parallel degree 8 (row slices of gate and
         # the head, a k slice of down): the kernels at their real shard shapes.
         plan += [("Q4_K shard", 12, 1792, 4096, 1, None), ("Q6_K shard", 14, 4096, 1792, 1, None),

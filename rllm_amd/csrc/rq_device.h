@@ -80,6 +80,16 @@ __device__ __forceinline__ int4 ld16_nt(const u8* p) {
     return make_int4(v.x, v.y, v.z, v.w);
 }
 
+// 4- and 8-byte forms of ld16_nt.
+__device__ __forceinline__ u32 ld4_nt(const u8* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32*)p);
+}
+__device__ __forceinline__ uint2 ld8_nt(const u8* p) {
+    typedef u32 v2u_nt __attribute__((ext_vector_type(2)));
+    const v2u_nt v = __builtin_nontemporal_load((const __attribute__((address_space(1))) v2u_nt*)p);
+    return make_uint2(v.x, v.y);
+}
+
 // ---------------------------------------------------------------------------
 // Q8_1 rounding. Numerics (bit-exact with the CPU restatement): d = amax / 127
 // and x / d are IEEE divisions (built with

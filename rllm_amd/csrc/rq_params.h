@@ -135,13 +135,24 @@ struct RqDotsParams {
 //               value 16 * (code - 8).
 //   Q8_0        block (T, w) = T * 4 * S2 + w for window w: byte b of lane
 //               (n, g) is the int8 code of element 64w + 16g + b.
+//   Q6_K        block (T, s, i) = T * 3 * S2 + 3 s + i for i = 0, 1, 2: with
+//               u = q XOR 32 for the 6-bit code q of an element, byte b of
+//               lane (n, g) holds in bits 7..2 the u of element 256s + 64i +
+//               16g + b (window i of the super-block) and in bits 1..0 bits
+//               2i + 1 .. 2i of the u of element 256s + 192 + 16g + b
+//               (window 3). Masking with 0xFC, or gathering window 3's three
+//               2-bit pieces into bits 7..2, gives the signed value 4 (q - 32).
 // Header plane, 256 B per (tile, super-block s): row n's 16 bytes at
 //   ((T * S2 + s) * 16 + n) * 16:
 //   Q4_K        GGUF bytes 0..15 of the super-block (f16 d, f16 dmin, the 12
 //               bytes of packed 6-bit scales and mins), verbatim;
-//   Q4_0, Q8_0  the f16 scales d of the super-block's eight 32-element blocks.
-// Bytes per row and super-block equal GGUF's (144 / 144 / 272): the repack
-// moves bits and rounds nothing.
+//   Q4_0, Q8_0  the f16 scales d of the super-block's eight 32-element blocks;
+//   Q6_K        the 16 int8 sub-block scales (GGUF bytes 192..207), verbatim.
+// Q6_K row scales follow the header plane (at hdr + tiles * S2 * 256): the
+//   f16 d of row 16T + n, super-block s at ((T * 16 + n) * DS + s) * 2, with
+//   DS = S2 rounded up to a multiple of 8 (a wave's d are one aligned load).
+// Bytes per row and super-block equal GGUF's (144 / 144 / 272 / 210, plus
+// the Q6_K d row padding): the repack moves bits and rounds nothing.
 
 // Super-blocks per wave of an rq_mmq launch (RqMmqParams.ks waves per tile).
 #define RQ_MMQ_SBW_MAX 4
@@ -168,12 +179,12 @@ struct RqMmqParams {
     int32_t ks;          // waves (k-parts) per tile
     int32_t tr;          // tiles per workgroup
     // Workgroup LDS (byte offsets, set by the host): staged activation codes
-    // (column a at a * kxp), a zero region of sbw * 256 bytes at z_off, the
-    // per-block activation planes at pl_off, the waves' partial sums at part_off.
+    // (column a at a * kxp), the per-block activation planes at pl_off, the
+    // waves' partial sums at part_off.
     int32_t kxp;
-    int32_t z_off;
     int32_t pl_off;
     int32_t part_off;
+    int32_t pad;
 };
 
 struct RqMmqRepackParams {
@@ -182,7 +193,9 @@ struct RqMmqRepackParams {
     uint8_t* hdr;
     int64_t row0;
     int64_t rows;
-    int32_t S2, k, pad[2];
+    int32_t S2, k;
+    int32_t tiles;  // of the whole weight (Q6_K: the row scales follow the header plane)
+    int32_t pad;
 };
 
 // ---------------------------------------------------------------------------
