@@ -87,11 +87,11 @@ rq_status rq_set_stream(rq_ctx* ctx, void* stream);
  *   RQ_KERNELS_AUTO  the dot4 kernels, the faster family at one activation
  *                    column (batch-1 decode) on MI355X (default);
  *   RQ_KERNELS_DOT4  v_dot4_i32_i8 kernels for every type;
- *   RQ_KERNELS_MFMA  int8-MFMA kernels (v_mfma_i32_16x16x64_i8) for Q4_0,
- *                    Q8_0 and Q4_K (faster from 4 activation columns up:
- *                    continuous batching), dot4 kernels for Q6_K.
- * Widths the MFMA kernels cannot stage (Q4_0 / Q4_K: cols > 32768, Q8_0:
- * cols > 16384) fall back to dot4. Both families compute the same int32 block
+ *   RQ_KERNELS_MFMA  int8-MFMA kernels (v_mfma_i32_16x16x64_i8) for every
+ *                    type (faster from 4 activation columns up: continuous
+ *                    batching).
+ * Widths the MFMA kernels cannot stage (Q4_0 / Q4_K: cols > 32768, Q8_0 /
+ * Q6_K: cols > 16384) fall back to dot4. Both families compute the same int32 block
  * dots; their f32 sums differ only in accumulation order. The environment
  * variable RQ_KERNELS=auto|dot4|mfma sets the default at rq_open. */
 #define RQ_KERNELS_AUTO 0
