@@ -108,6 +108,8 @@ constexpr size_t kUploadChunkBytes = size_t(16) << 20;
 constexpr int kLdsBudget = 64 << 10;
 // LDS bytes per activation column per super-block column (RQ_LDS_REC in rq_kernels.hip).
 constexpr int kLdsPerSb = 400;
+// Most waves of a dot4 matvec launch whose rows are split into k-parts.
+constexpr int64_t kKpMaxWaves = 4096;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -205,9 +207,10 @@ struct rq_ctx {
     hipModule_t mod = nullptr;
     hipFunction_t quant = nullptr;
     int lds_wide = 0;  // LDS bytes a wide matvec workgroup may use
-    // [0]: 256-thread workgroups, [1]: RQ_MV_WIDE_THREADS(fmt)-thread workgroups.
-    hipFunction_t mvx[2][RQ_NUM_FMTS][RQ_MV_MAX_NC + 1] = {};  // Q8_1 activations
-    hipFunction_t mvf[2][RQ_NUM_FMTS] = {};                    // one f32 column, quantized while staging
+    // [0]: 256-thread workgroups, [1]: RQ_MV_WIDE_THREADS(fmt)-thread
+    // workgroups, [2]: the same with rows split into k-parts (RqTiled.P).
+    hipFunction_t mvx[3][RQ_NUM_FMTS][RQ_MV_MAX_NC + 1] = {};  // Q8_1 activations
+    hipFunction_t mvf[3][RQ_NUM_FMTS] = {};                    // one f32 column, quantized while staging
     // Q8_1 scratch of rq_matmul / rq_matmul_many for m >= 2 (grown on
     // demand, or sized up front by rq_reserve).
     int8_t* sq = nullptr;
@@ -307,6 +310,9 @@ void tile_geometry(int64_t rows, int64_t cols, RqTiled& t) {
     while (sp < t.S) sp *= 2;
     t.R = t.S <= 32 ? 64 / sp : 1;
     t.T = (int32_t)((rows + t.R - 1) / t.R);
+    // Wider than 64 super-blocks: 2 or 4 waves per row in the matvec
+    // launches that split rows (matvec_launch decides per launch).
+    t.P = t.S > 128 ? 4 : (t.S > 64 ? 2 : 1);
 }
 
 // Most activation columns a matvec workgroup can stage for S super-blocks
@@ -332,25 +338,64 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
     const int fmt = ws[0]->fmt;
     bool mixed = false;
     for (int i = 1; i < count; i++) mixed |= ws[i]->fmt != fmt;
+    // k-parts (waves per tile; every target has the same k): only in launches
+    // of at most kKpMaxWaves waves. There a second, serial pass over a row's
+    // super-blocks is latency the few waves cannot hide (measured, 1 to 4
+    // columns: Q6_K 1024 x 40960 10.1 / 19.4 / 38.8 us -> 9.5 / 12.1 / 23.6,
+    // Q8_0 1024 x 36864 12.0 / 18.4 / 36.8 -> 9.1 / 14.2 / 28.1, Q6_K 2048 x
+    // 20480 9.4 / 14.8 / 19.2 -> 9.3 / 11.3 / 14.8); larger launches hide it,
+    // and doubling their waves and staging costs more (Q6_K 8192 x 28672:
+    // 34.6 -> 38.0 us).
+    int64_t launch_rows = 0;
+    for (int i = 0; i < count; i++) launch_rows += ws[i]->rows;
+    const int kp = launch_rows * ws[0]->tiled.P <= kKpMaxWaves ? ws[0]->tiled.P : 1;
+    if (mixed && kp > 1) {
+        // The mixed-format kernels take one wave per tile: one launch per format.
+        for (const int f : {RQ_FMT_Q4_K, RQ_FMT_Q6_K}) {
+            const rq_weight* wf[RQ_MV_TARGETS];
+            float* of[RQ_MV_TARGETS];
+            int nf = 0;
+            for (int i = 0; i < count; i++) {
+                if (ws[i]->fmt != f) continue;
+                wf[nf] = ws[i];
+                of[nf++] = outs[i];
+            }
+            const rq_status st = nf ? matvec_launch(ctx, xq, xd, xf, m, wf, of, nf) : RQ_OK;
+            if (st != RQ_OK) return st;
+        }
+        return RQ_OK;
+    }
     const int64_t k = ws[0]->cols, U = (k + 31) / 32;
     const int S = ws[0]->tiled.S;
-    const int wide = mv_wide(ws[0]->tiled.R, m, xf != nullptr) ? 1 : 0;
-    const int waves_per_wg = wide ? RQ_MV_WIDE_THREADS(fmt) / 64 : RQ_WAVES;
-    const int group = mvx_max_cols(S, wide ? ctx->lds_wide : kLdsBudget);
+    // Wide workgroups also for k-parts (a 256-thread workgroup would stage
+    // the whole activation for one or two rows) and when one column's staging
+    // needs more LDS than a 256-thread workgroup may use (S > 163).
+    const int wide =
+        mv_wide(ws[0]->tiled.R, m, xf != nullptr) || kp > 1 || mvx_max_cols(S, kLdsBudget - 512) < 1 ? 1 : 0;
+    // Waves per workgroup of a launch of nc columns.
+    auto wg_waves = [&](int nc) {
+        if (!wide) return RQ_WAVES;
+        return (mixed && !xf ? RQ_MVXM_WIDE_THREADS(nc) : RQ_MV_WIDE_THREADS(fmt)) / 64;
+    };
+    // k-parts leave one float per wave and column after the staged records.
+    const int part_lds = kp > 1 ? wg_waves(1) * RQ_MV_MAX_NC * 4 : 0;
+    const int group = mvx_max_cols(S, (wide ? ctx->lds_wide : kLdsBudget) - part_lds);
     if (group < 1) return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage", (long long)k);
     const int64_t ngroups = (m + group - 1) / group;
     for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
         const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
+        const int waves_per_wg = wg_waves(nc);
         RqMvParams p;
         memset(&p, 0, sizeof p);
         int64_t waves = 0;
         for (int i = 0; i < count; i++) {
             const rq_weight* w = ws[i];
             p.t[i].w = w->tiled;
+            p.t[i].w.P = kp;
             p.t[i].out = outs[i] + g0 * w->rows;
             p.t[i].n = (int32_t)w->rows;
             p.t[i].wave_start = (int32_t)waves;
-            waves += w->tiled.T;
+            waves += (int64_t)w->tiled.T * kp;
         }
         if (xf) {
             p.xf = xf + g0 * k;
@@ -361,9 +406,11 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
         p.count = count;
         p.m = nc;
         const uint64_t blocks = (uint64_t)((waves + waves_per_wg - 1) / waves_per_wg);
+        const int v = kp > 1 ? 2 : wide;  // the k-part kernels are wide
         hipFunction_t f = mixed ? (xf ? ctx->mvfm[wide] : ctx->mvxm[wide][nc])
-                                : (xf ? ctx->mvf[wide][fmt] : ctx->mvx[wide][fmt][nc]);
-        rq_status st = launch(ctx, f, xf ? "rq_mvf" : "rq_mvx", blocks, &p, (unsigned)(nc * kLdsPerSb * S),
+                                : (xf ? ctx->mvf[v][fmt] : ctx->mvx[v][fmt][nc]);
+        rq_status st = launch(ctx, f, xf ? "rq_mvf" : "rq_mvx", blocks, &p,
+                              (unsigned)(nc * kLdsPerSb * S + (kp > 1 ? waves_per_wg * nc * 4 : 0)),
                               (unsigned)(64 * waves_per_wg));
         if (st != RQ_OK) return st;
         g0 += nc;
@@ -818,15 +865,16 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     }
     char name[64];
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
+        static const char* const kVariant[3] = {"", "w", "k"};
         for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {
-            for (int wide = 0; wide < 2 && st == RQ_OK; wide++) {
-                snprintf(name, sizeof name, "rq_mvx%s_%s_%d", wide ? "w" : "", kFmtSuffix[f], nc);
-                st = get(&ctx->mvx[wide][f][nc], name);
+            for (int v = 0; v < 3 && st == RQ_OK; v++) {
+                snprintf(name, sizeof name, "rq_mvx%s_%s_%d", kVariant[v], kFmtSuffix[f], nc);
+                st = get(&ctx->mvx[v][f][nc], name);
             }
         }
-        for (int wide = 0; wide < 2 && st == RQ_OK; wide++) {
-            snprintf(name, sizeof name, "rq_mvf%s_%s", wide ? "w" : "", kFmtSuffix[f]);
-            st = get(&ctx->mvf[wide][f], name);
+        for (int v = 0; v < 3 && st == RQ_OK; v++) {
+            snprintf(name, sizeof name, "rq_mvf%s_%s", kVariant[v], kFmtSuffix[f]);
+            st = get(&ctx->mvf[v][f], name);
         }
         if (st != RQ_OK) break;
         for (int nc = 1; nc <= RQ_MV_MAX_NC && st == RQ_OK; nc++) {

@@ -10,6 +10,7 @@
 //   rq_mvx_<fmt>_<nc>    matvec over nc = 1..8 Q8_1 activation columns (staged in LDS)
 //   rq_mvf_<fmt>         one f32 activation column, quantized while staging
 //   rq_mvxw_*, rq_mvfw_* the same with 1024-thread (Q8_0: 512) workgroups (tiles of < 4 rows)
+//   rq_mvxk_*, rq_mvfk_* wide, rows of more than 64 super-blocks split over 2 or 4 waves
 //   rq_mvxm_q4_k_q6_k_<nc>, rq_mvfm_q4_k_q6_k (+ w) launches mixing Q4_K and Q6_K targets
 //   rq_glu_<fmt>_<nc>    gated FFN front half act(gate . x) * (up . x) + its Q8_1 (rq_gluf_*: f32 x)
 //   rq_act_mul           elementwise act(g) * u, optionally with Q8_1 of the result
@@ -315,7 +316,9 @@ struct TileLane {
     bool real;  // a slot of the row, not padding
 };
 
-__device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane) {
+// part: the wave's k-part of an R = 1 tile split over several waves (its
+// first super-block is 64 part; padding lanes re-read that one).
+__device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane, int part = 0) {
     TileLane r;
     if (w.R > 1) {
         const int sh = __builtin_ctz(64 / w.R);  // log2(Sp)
@@ -325,8 +328,8 @@ __device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane) {
         if (!r.real) r.col = 0;
     } else {
         r.row = 0;
-        r.real = lane < w.S;
-        r.col = r.real ? lane : 0;
+        r.real = 64 * part + lane < w.S;
+        r.col = 64 * part + (r.real ? lane : 0);
     }
     r.slot = r.row * w.S + r.col;
     return r;
@@ -575,15 +578,17 @@ __device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
     RQ_PICK(w.T)
     RQ_PICK(w.k)
     RQ_PICK(w.fmt)
+    RQ_PICK(w.P)
     RQ_PICK(out)
     RQ_PICK(n)
     RQ_PICK(wave_start)
 #undef RQ_PICK
-    r.w.pad = 0;
     return r;
 }
 
-template <int FMT, int NC, bool F32IN, int WAVES>
+// KP: the k-part variant (rq_mvxk_* / rq_mvfk_*, launched only for rows of
+// more than 64 super-blocks); without it, w.P is ignored.
+template <int FMT, int NC, bool F32IN, int WAVES, bool KP = false>
 __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     const int lane = threadIdx.x & 63;
     const int gwave = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -595,32 +600,63 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // By value (a reference indexed by ti reloads its fields with dependent
     // scalar loads at each use).
     const RqMvTarget T = pick_target(P, ti);
-    const int t = gwave - T.wave_start;  // this wave's tile
-    const bool has_tile = t < T.w.T;     // wave-uniform
+    // Rows wider than 64 super-blocks (R = 1) are split over kp = 2 or 4
+    // waves of one workgroup: wave `part` of a tile takes super-blocks 64
+    // part .. 64 part + 63 (then every 64 kp-th further on), all loaded up
+    // front, and the parts' sums meet in LDS in a fixed order.
+    const int kp = KP ? T.w.P : 1;  // wave-uniform: 1, 2 or 4
+    const int lkp = kp == 4 ? 2 : kp >> 1;  // log2(kp)
+    const int t = (gwave - T.wave_start) >> lkp;  // this wave's tile
+    const int part = (gwave - T.wave_start) & (kp - 1);
+    const bool has_tile = t < T.w.T;  // wave-uniform
+    // Waves past the last tile (only in k-part launches do they go on, to
+    // the barrier) work on the last tile and store nothing.
+    const int tc = has_tile ? t : T.w.T - 1;
     const int slots = T.w.R * S;  // stored slots per tile
-    const TileLane tl = tile_lane(T.w, lane);
+    const TileLane tl = tile_lane(T.w, lane, part);
     const RowDst dst = row_dst(T, t, lane);
 
-    // The tile's weight loads (clamped to a valid tile; waves without one
-    // discard it) go out right behind round 0 of the staging loads.
+    // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
-    stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
-                                         [&] { load_sb<FMT>(T.w, has_tile ? t : T.w.T - 1, tl.slot, w); });
-    if (!has_tile) return;  // wave-uniform; no barrier follows
+    stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] { load_sb<FMT>(T.w, tc, tl.slot, w); });
+    if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
 
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = 0.f;
     slot_dot<FMT, NC>(w, S, tl.col, tl.real, acc);
-    // Rows wider than 64 super-blocks: further slot passes (R = 1).
-    for (int a = lane + 64; a - lane < slots; a += 64) {
+    // Rows wider than 64 kp super-blocks: further slot passes (R = 1).
+    for (int a0 = 64 * (part + kp); a0 < slots; a0 += 64 * kp) {
+        const int a = a0 + lane;
         const bool active = a < slots;
         SB<FMT> w2;
-        load_sb<FMT>(T.w, t, active ? a : 0, w2);
+        load_sb<FMT>(T.w, tc, active ? a : 0, w2);
         slot_dot<FMT, NC>(w2, S, active ? a : 0, active, acc);
     }
+    // Row sums: stored, or with k-parts left in LDS (wave w of the workgroup
+    // at part_lds[w][c], after the staged records) for the tile's part-0
+    // wave, which adds its kp waves' sums in part order and stores.
+    float* part_lds = (float*)(rq_lds + (size_t)NC * S * RQ_LDS_REC);
+    const int wv = threadIdx.x >> 6;
 #pragma unroll
-    for (int c = 0; c < NC; c++) tile_store(dst, T.n, acc[c], c);
+    for (int c = 0; c < NC; c++) {
+        const float v = group_sum(acc[c], dst.g);
+        if (kp == 1) {
+            if (dst.store) gmem(dst.out)[(int64_t)c * T.n] = v;
+        } else if (lane == 0) {
+            part_lds[wv * NC + c] = v;
+        }
+    }
+    if (kp == 1) return;
+    __syncthreads();
+    if (part == 0 && dst.store) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float v = part_lds[wv * NC + c];
+            for (int q = 1; q < kp; q++) v += part_lds[(wv + q) * NC + c];
+            gmem(dst.out)[(int64_t)c * T.n] = v;
+        }
+    }
 }
 
 #define RQ_MVX(NAME, FMT, NC)                                                                                         \
@@ -629,6 +665,9 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     }                                                                                                                 \
     extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvxw_##NAME##_##NC(RqMvParams p) {       \
         mvx_body<FMT, NC, false, RQ_MV_WIDE_THREADS(FMT) / 64>(p);                                                    \
+    }                                                                                                                 \
+    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvxk_##NAME##_##NC(RqMvParams p) {       \
+        mvx_body<FMT, NC, false, RQ_MV_WIDE_THREADS(FMT) / 64, true>(p);                                              \
     }
 
 // f32 activations: one column (rq_matmul with m == 1).
@@ -638,6 +677,9 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     }                                                                                                                 \
     extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvfw_##NAME(RqMvParams p) {              \
         mvx_body<FMT, 1, true, RQ_MV_WIDE_THREADS(FMT) / 64>(p);                                                      \
+    }                                                                                                                 \
+    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(FMT)) void rq_mvfk_##NAME(RqMvParams p) {              \
+        mvx_body<FMT, 1, true, RQ_MV_WIDE_THREADS(FMT) / 64, true>(p);                                                \
     }
 
 // Launches whose targets mix Q4_K and Q6_K weights of one width (q, k and v
@@ -704,9 +746,8 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_mvxm_q4_k_q6_k_##NC(RqMvParams p) {                   \
         mvx_mix_body<NC, false, RQ_WAVES>(p);                                                                         \
     }                                                                                                                 \
-    extern "C" __global__ __launch_bounds__(RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K)) void rq_mvxmw_q4_k_q6_k_##NC(            \
-        RqMvParams p) {                                                                                               \
-        mvx_mix_body<NC, false, RQ_MV_WIDE_THREADS(RQ_FMT_Q4_K) / 64>(p);                                             \
+    extern "C" __global__ __launch_bounds__(RQ_MVXM_WIDE_THREADS(NC)) void rq_mvxmw_q4_k_q6_k_##NC(RqMvParams p) {    \
+        mvx_mix_body<NC, false, RQ_MVXM_WIDE_THREADS(NC) / 64>(p);                                                    \
     }
 RQ_MVXM(1)
 RQ_MVXM(2)

@@ -56,6 +56,12 @@ static inline int rq_chunks(int fmt) { return fmt == RQ_FMT_Q8_0 ? 17 : (fmt == 
 // (68 registers) of weights per lane and does not fit the 128 registers a
 // wave of a 1024-thread workgroup may use, so its wide workgroups have 512.
 #define RQ_MV_WIDE_THREADS(fmt) ((fmt) == RQ_FMT_Q8_0 ? 512 : 1024)
+// The same for launches mixing Q4_K and Q6_K targets (rq_mvxmw_*): their
+// register block is Q6_K's, which with the sums of three or more columns does
+// not fit 128 registers either (measured, q/k/v of width 5120 at 4 and 8
+// columns: 18.9 and 40.8 us spilling in 1024-thread workgroups, 13.6 and
+// 20.0 us in 512; at 2 columns the small spill costs less, 9.8 against 10.2).
+#define RQ_MVXM_WIDE_THREADS(nc) ((nc) >= 3 ? 512 : 1024)
 // Weights sharing one activation in one launch (Q/K/V, gate/up).
 #define RQ_MV_TARGETS 3
 // Most activation columns per matvec launch.
@@ -69,7 +75,7 @@ struct RqTiled {
     int32_t T;            // tiles
     int32_t k;            // columns
     int32_t fmt;          // RQ_FMT_* (chosen per wave in mixed launches)
-    int32_t pad;
+    int32_t P;            // waves per tile in rq_mvx_* / rq_mvf_*: 1, or 2 / 4 (S > 64) in small launches
 };
 
 struct RqMvTarget {

@@ -152,6 +152,56 @@ def test_odd_widths(gpuk, orc, tname, k, m):
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("k", [256 * 65, 17408, 32768, 256 * 129, 40960, 256 * 170])
+@pytest.mark.parametrize("m", [1, 2, 9])
+def test_wide_rows_k_parts(gpu, orc, tname, k, m):
+    """Rows of S = 65, 68, 128, 129, 160 and 170 super-blocks: the dot4
+    matvec splits each over 2 (S <= 128) or 4 waves of one workgroup whose
+    sums meet in LDS; 37 rows leave the last workgroup with waves past the
+    last row. Block dots bit-exact, f32 within the bars (Q8_1 and f32 entry
+    points), and the result does not depend on the launch's column count."""
+    t, n = TYPES[tname], 37
+    w = make_weight(orc, t, n, k, 5 * k + m, "random")
+    wg = upload(gpu, t, w, n, k)
+    assert wg.kernels == "dot4"
+    x = _x(orc, 11 + k + m, m, k)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    xq = q8_1_to_device(gpu, qs, d, s)
+    want = orc.matvec_q8_1(t, w, n, k, qs, d, m)
+    out = gpu.alloc(m * n)
+    gpu.matvec(xq, wg, out, m)
+    got = gpu.to_host(out, m * n)
+    orc.assert_close(f"{tname} k={k} m={m} matvec", want, got, TOL_B)
+    out2 = gpu.alloc(m * n)
+    gpu.matmul(gpu.from_host(x), wg, out2, m)
+    orc.assert_close(f"{tname} k={k} m={m} matmul", want, gpu.to_host(out2, m * n), TOL_B)
+    if m == 2:
+        assert np.array_equal(gpu.block_dots(xq, wg, m).cpu().numpy(), orc.block_dots(t, w, n, k, qs, m))
+        # Column 1 alone: the same bits as within the two-column launch.
+        one = gpu.alloc(n)
+        q1 = q8_1_to_device(gpu, qs[k:], d[k // 32:], s[k // 32:])
+        gpu.matvec(q1, wg, one, 1)
+        assert np.array_equal(gpu.to_host(one, n).view(np.uint32), got[n:].view(np.uint32))
+
+
+@pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("k", [17408, 256 * 129])
+@pytest.mark.parametrize("m", [1, 3])
+def test_wide_rows_large_launch(gpu, orc, tname, k, m):
+    """2100 rows of S = 68 or 129 super-blocks: more waves than the k-part
+    split allows (rows x parts > 4096), so one wave walks each row in serial
+    passes of 64 super-blocks."""
+    t, n = TYPES[tname], 2100
+    w = make_weight(orc, t, n, k, 3 * k + m, "random")
+    wg = upload(gpu, t, w, n, k)
+    x = _x(orc, 21 + k + m, m, k)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    out = gpu.alloc(m * n)
+    gpu.matvec(q8_1_to_device(gpu, qs, d, s), wg, out, m)
+    orc.assert_close(f"{tname} {n}x{k} m={m}", orc.matvec_q8_1(t, w, n, k, qs, d, m), gpu.to_host(out, m * n), TOL_B)
+
+
+@pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("n,k", [(1, 256), (5, 256), (130, 2048), (257, 4096), (40, 14336)])
 def test_matvec_shapes(gpuk, orc, tname, n, k):
     t = TYPES[tname]
