@@ -184,6 +184,40 @@ def test_wide_rows_k_parts(gpu, orc, tname, k, m):
         assert np.array_equal(gpu.to_host(one, n).view(np.uint32), got[n:].view(np.uint32))
 
 
+@pytest.mark.parametrize("family", ["dot4", "mfma"])
+def test_weight_over_2gib(gpu, orc, family):
+    """A Q8_0 weight of 2.28 GB (524288 x 4096): byte offsets past 2^31 in
+    the upload chunks, the repack and the matvec loads. The rows are a tiled
+    16 MiB block except two distinct slices, one across the 2^31-byte mark
+    (row 493448) and the last 64 rows, which are checked against the oracle."""
+    t, n, k, m = 8, 524288, 4096, 3
+    rb = orc.row_bytes(t, k)
+    base_rows = (16 << 20) // rb
+    w = np.empty(n * rb, dtype=np.uint8)
+    block = orc.random_weight(71, t, base_rows, k)
+    for r0 in range(0, n, base_rows):
+        r1 = min(n, r0 + base_rows)
+        w[r0 * rb:r1 * rb] = block[:(r1 - r0) * rb]
+    slices = [(493400, 493500), (n - 64, n)]
+    for i, (a, b) in enumerate(slices):
+        w[a * rb:b * rb] = orc.random_weight(72 + i, t, b - a, k)
+    gpu.set_kernels(family)
+    try:
+        wg = upload(gpu, t, w, n, k)
+    finally:
+        gpu.set_kernels("auto")
+    assert wg.kernels == family
+    x = _x(orc, 73, m, k)
+    qs, d, s = orc.quantize_q8_1(x, m, k)
+    out = gpu.alloc(m * n)
+    gpu.matvec(q8_1_to_device(gpu, qs, d, s), wg, out, m)
+    got = gpu.to_host(out, m * n).reshape(m, n)
+    for a, b in slices:
+        want = orc.matvec_q8_1(t, w[a * rb:b * rb], b - a, k, qs, d, m).reshape(m, b - a)
+        orc.assert_close(f"{family} rows {a}..{b}", want.reshape(-1), got[:, a:b].reshape(-1), TOL_B)
+    wg.free()
+
+
 @pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("k", [17408, 256 * 129])
 @pytest.mark.parametrize("m", [1, 3])
