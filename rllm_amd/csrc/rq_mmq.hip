@@ -426,6 +426,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
         const int a_lane = MP == 1 ? 0 : MP == 2 ? (g >> 1) : MP == 4 ? g : 2 * g;
         const int lb_lane = MP == 1 ? 4 * g : MP == 2 ? 4 * (g & 1) : 0;
         const char* plb = mmq_lds + P.pl_off + (a_lane * NB + sb0 * 8 + lb_lane) * 4;
+        float sbd[2] = {0.f, 0.f}, sbm[2] = {0.f, 0.f};  // Q4_K: the current super-block's sums
 #pragma unroll
         for (int t = 0; t < ND; t++) {
             if (t * NPH * 64 >= nsb * 256) break;  // a short last k-part (uniform)
@@ -496,16 +497,20 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                 if (FMT == RQ_FMT_Q4_K) {
                     const float4 p1 = *(const float4*)(plb + 4 * lbo + stride);
                     const float pv1[4] = {p1.x, p1.y, p1.z, p1.w};
-                    float accd = 0.f, accm = 0.f;
+                    // mp = 4: a super-block spans D-groups 2i, 2i + 1; its d
+                    // and dmin apply once, after both.
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         const bool hiw = (v >> 1) & 1;
                         const float tv = hiw ? fmaf(pv0[v], (float)D[v], pv1[v]) : pv0[v] * (float)D[v];
-                        accd = fmaf(byte_f(sc.sc, v), tv, accd);
-                        accm = fmaf(byte_f(sc.mn, v), pv1[v], accm);
+                        sbd[0] = fmaf(byte_f(sc.sc, v), tv, sbd[0]);
+                        sbm[0] = fmaf(byte_f(sc.mn, v), pv1[v], sbm[0]);
                     }
-                    y[gi][0] = fmaf(sc.d, accd, y[gi][0]);
-                    y[gi][0] = fmaf(-0.125f * sc.dmin, accm, y[gi][0]);
+                    if (MP != 4 || (t & 1) == 1) {
+                        y[gi][0] = fmaf(sc.d, sbd[0], y[gi][0]);
+                        y[gi][0] = fmaf(-0.125f * sc.dmin, sbm[0], y[gi][0]);
+                        sbd[0] = sbm[0] = 0.f;
+                    }
                 } else if (FMT == RQ_FMT_Q4_0) {
                     const float4 p1 = *(const float4*)(plb + 4 * lbo + stride);
                     const float pv1[4] = {p1.x, p1.y, p1.z, p1.w};
@@ -527,18 +532,22 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                     const float2 p0 = *(const float2*)pe;
                     const float pv0[2] = {p0.x, p0.y};
                     if (FMT == RQ_FMT_Q4_K) {
+                        // The super-block's d and dmin apply once, after its
+                        // four windows (D-groups t = 4i .. 4i + 3).
                         const float2 p1 = *(const float2*)(pe + stride);
                         const float pv1[2] = {p1.x, p1.y};
                         const int bsh = jb & 3;  // byte of block jb in its scale word
-                        float accd = 0.f, accm = 0.f;
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
                             const float tv = hiw ? fmaf(pv0[h], (float)D[2 * e + h], pv1[h]) : pv0[h] * (float)D[2 * e + h];
-                            accd = fmaf(byte_f(sc.sc, bsh + h), tv, accd);
-                            accm = fmaf(byte_f(sc.mn, bsh + h), pv1[h], accm);
+                            sbd[e] = fmaf(byte_f(sc.sc, bsh + h), tv, sbd[e]);
+                            sbm[e] = fmaf(byte_f(sc.mn, bsh + h), pv1[h], sbm[e]);
                         }
-                        y[gi][e] = fmaf(sc.d, accd, y[gi][e]);
-                        y[gi][e] = fmaf(-0.125f * sc.dmin, accm, y[gi][e]);
+                        if ((t & 3) == 3) {
+                            y[gi][e] = fmaf(sc.d, sbd[e], y[gi][e]);
+                            y[gi][e] = fmaf(-0.125f * sc.dmin, sbm[e], y[gi][e]);
+                            sbd[e] = sbm[e] = 0.f;
+                        }
                     } else if (FMT == RQ_FMT_Q4_0) {
                         const float2 p1 = *(const float2*)(pe + stride);
                         const float pv1[2] = {p1.x, p1.y};
