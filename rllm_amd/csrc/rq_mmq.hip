@@ -288,20 +288,25 @@ __device__ __forceinline__ void mmq_stage(const RqMmqParams& P, int gi, const XB
     __syncthreads();
 }
 
-// The tile's sums, in a fixed order: first the lanes of one (row,
-// activation) within a wave (mp = 1: four k-groups), then the k-parts in LDS.
-template <int MP, int G, int NACC>
-__device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarget& T, float (&y)[G][NACC]) {
-    const int threads = blockDim.x, tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int blk = blockIdx.x, ks = P.ks;
-    if (MP <= 2) y[0][0] += __shfl_xor(y[0][0], 16);
-    if (MP == 1) y[0][0] += __shfl_xor(y[0][0], 32);
+// A column group's sums of the lane: first added over the lanes of one
+// (row, activation) within the wave (mp = 1: four k-groups), then left in LDS
+// for mmq_reduce (wave w, group gi at slot w * G + gi); only the current
+// group's sums live in registers.
+template <int MP, int NACC>
+__device__ __forceinline__ void mmq_part_store(const RqMmqParams& P, float (&y)[NACC], int slot, int lane) {
+    if (MP <= 2) y[0] += __shfl_xor(y[0], 16);
+    if (MP == 1) y[0] += __shfl_xor(y[0], 32);
     float* part = (float*)(mmq_lds + P.part_off);
 #pragma unroll
-    for (int gi = 0; gi < G; gi++)
-#pragma unroll
-        for (int e = 0; e < NACC; e++) part[((wave * G + gi) * 64 + lane) * NACC + e] = y[gi][e];
+    for (int e = 0; e < NACC; e++) part[(slot * 64 + lane) * NACC + e] = y[e];
+}
+
+// The tile's sums, in a fixed order: the k-parts' partial sums in LDS.
+template <int MP, int G, int NACC>
+__device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarget& T) {
+    const int threads = blockDim.x, tid = threadIdx.x;
+    const int blk = blockIdx.x, ks = P.ks;
+    const float* part = (const float*)(mmq_lds + P.part_off);
     __syncthreads();
     float* out = (float*)T.out;
     for (int it = tid; it < P.tr * G * MP * 16; it += threads) {
@@ -396,15 +401,12 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- Staging writes (the LDS writes wait only for the staging loads).
-    float y[G][NACC];
-#pragma unroll
-    for (int gi = 0; gi < G; gi++)
-#pragma unroll
-        for (int e = 0; e < NACC; e++) y[gi][e] = 0.f;
-
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
     mmq_stage<FMT, MP, F32IN, DOTS>(P, gi, x0, q0);
+    float y[NACC];
+#pragma unroll
+    for (int e = 0; e < NACC; e++) y[e] = 0.f;
 
     if (has_tile) {
         // A operand: row ia = lane % 16 of A is (activation ia / PS, slot ia % PS);
@@ -507,8 +509,8 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                         sbm[0] = fmaf(byte_f(sc.mn, v), pv1[v], sbm[0]);
                     }
                     if (MP != 4 || (t & 1) == 1) {
-                        y[gi][0] = fmaf(sc.d, sbd[0], y[gi][0]);
-                        y[gi][0] = fmaf(-0.125f * sc.dmin, sbm[0], y[gi][0]);
+                        y[0] = fmaf(sc.d, sbd[0], y[0]);
+                        y[0] = fmaf(-0.125f * sc.dmin, sbm[0], y[0]);
                         sbd[0] = sbm[0] = 0.f;
                     }
                 } else if (FMT == RQ_FMT_Q4_0) {
@@ -517,12 +519,12 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         const float tv = fmaf(pv0[v], (float)D[v], pv1[v]);
-                        y[gi][0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), tv, y[gi][0]);
+                        y[0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), tv, y[0]);
                     }
                 } else {
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        y[gi][0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), pv0[v] * (float)D[v], y[gi][0]);
+                        y[0] = fmaf(half_f(v < 2 ? sc.dw0 : sc.dw1, v & 1), pv0[v] * (float)D[v], y[0]);
                 }
             } else {  // mp = 8: two activations per lane, blocks pb, pb + 1
                 const bool hiw = t & 1;
@@ -544,8 +546,8 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                             sbm[e] = fmaf(byte_f(sc.mn, bsh + h), pv1[h], sbm[e]);
                         }
                         if ((t & 3) == 3) {
-                            y[gi][e] = fmaf(sc.d, sbd[e], y[gi][e]);
-                            y[gi][e] = fmaf(-0.125f * sc.dmin, sbm[e], y[gi][e]);
+                            y[e] = fmaf(sc.d, sbd[e], y[e]);
+                            y[e] = fmaf(-0.125f * sc.dmin, sbm[e], y[e]);
                             sbd[e] = sbm[e] = 0.f;
                         }
                     } else if (FMT == RQ_FMT_Q4_0) {
@@ -554,20 +556,21 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
                             const float tv = fmaf(pv0[h], (float)D[2 * e + h], pv1[h]);
-                            y[gi][e] = fmaf(half_f(sc.dw0, h), tv, y[gi][e]);
+                            y[e] = fmaf(half_f(sc.dw0, h), tv, y[e]);
                         }
                     } else {
 #pragma unroll
                         for (int h = 0; h < 2; h++)
-                            y[gi][e] = fmaf(half_f(sc.dw0, h), pv0[h] * (float)D[2 * e + h], y[gi][e]);
+                            y[e] = fmaf(half_f(sc.dw0, h), pv0[h] * (float)D[2 * e + h], y[e]);
                     }
                 }
             }
         }
     }
+    if (!DOTS) mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
     }  // column groups
     if (DOTS) return;
-    mmq_reduce<MP, G, NACC>(P, T, y);
+    mmq_reduce<MP, G, NACC>(P, T);
 }
 
 // ---------------------------------------------------------------------------
@@ -675,15 +678,12 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    float y[G][NACC];
-#pragma unroll
-    for (int gi = 0; gi < G; gi++)
-#pragma unroll
-        for (int e = 0; e < NACC; e++) y[gi][e] = 0.f;
-
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
     mmq_stage<FMT, MP, F32IN, DOTS>(P, gi, x0, q0);
+    float y[NACC];
+#pragma unroll
+    for (int e = 0; e < NACC; e++) y[e] = 0.f;
 
     if (has_tile) {
         // A row ia = lane % 16 and the phase the lane is live in (-1: none):
@@ -787,16 +787,17 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
                 }
             }
 #pragma unroll
-            for (int e = 0; e < NACC; e++) y[gi][e] = fmaf(dsb, acc[e], y[gi][e]);
+            for (int e = 0; e < NACC; e++) y[e] = fmaf(dsb, acc[e], y[e]);
         }
+    }
+    if (!DOTS) {
+#pragma unroll
+        for (int e = 0; e < NACC; e++) y[e] *= 0.25f;
+        mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
     }
     }  // column groups
     if (DOTS) return;
-#pragma unroll
-    for (int gi = 0; gi < G; gi++)
-#pragma unroll
-        for (int e = 0; e < NACC; e++) y[gi][e] *= 0.25f;
-    mmq_reduce<MP, G, NACC>(P, T, y);
+    mmq_reduce<MP, G, NACC>(P, T);
 }
 
 // Kernel bodies by format.
