@@ -89,14 +89,17 @@ rq_status rq_set_stream(rq_ctx* ctx, void* stream);
  *   RQ_KERNELS_DOT4  v_dot4_i32_i8 kernels for every type;
  *   RQ_KERNELS_MFMA  int8-MFMA kernels (v_mfma_i32_16x16x64_i8) for every
  *                    type (faster from 4 activation columns up: continuous
- *                    batching).
+ *                    batching);
+ *   RQ_KERNELS_BOTH  both layouts (twice the device memory): each call runs
+ *                    dot4 below 4 activation columns and MFMA from 4 up.
  * Widths the MFMA kernels cannot stage (Q4_0 / Q4_K: cols > 32768, Q8_0 /
  * Q6_K: cols > 16384) fall back to dot4. Both families compute the same int32 block
  * dots; their f32 sums differ only in accumulation order. The environment
- * variable RQ_KERNELS=auto|dot4|mfma sets the default at rq_open. */
+ * variable RQ_KERNELS=auto|dot4|mfma|both sets the default at rq_open. */
 #define RQ_KERNELS_AUTO 0
 #define RQ_KERNELS_DOT4 1
 #define RQ_KERNELS_MFMA 2
+#define RQ_KERNELS_BOTH 3
 
 /* Sets the kernel family for later rq_upload calls (tuning and tests; the
  * reference has one kernel family, so this has no counterpart there). */
@@ -122,8 +125,9 @@ rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols, const voi
 /* Frees the weight's device memory (stream-ordered after pending work). */
 rq_status rq_weight_free(rq_weight* w);
 rq_status rq_weight_shape(const rq_weight* w, int* type, int64_t* rows, int64_t* cols, size_t* device_bytes);
-/* The kernel family the weight was laid out for (RQ_KERNELS_DOT4 or
- * RQ_KERNELS_MFMA); no reference counterpart. */
+/* The kernel family the weight was laid out for (RQ_KERNELS_DOT4,
+ * RQ_KERNELS_MFMA, or RQ_KERNELS_BOTH for both layouts); no reference
+ * counterpart. */
 rq_status rq_weight_kernels(const rq_weight* w, int* family);
 /* Inverse of rq_upload's repack: writes the weight back as GGUF bytes to
  * host memory (debugging and round-trip tests; no reference counterpart). */

@@ -22,8 +22,8 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "rq.h")
 RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID, RQ_ERR_GGUF = 0, 1, 2, 3, 4, 5
 MATVEC_MAX_COLS = 8
 # Kernel families (rq_set_kernels).
-KERNELS_AUTO, KERNELS_DOT4, KERNELS_MFMA = 0, 1, 2
-KERNEL_FAMILIES = {"auto": KERNELS_AUTO, "dot4": KERNELS_DOT4, "mfma": KERNELS_MFMA}
+KERNELS_AUTO, KERNELS_DOT4, KERNELS_MFMA, KERNELS_BOTH = 0, 1, 2, 3
+KERNEL_FAMILIES = {"auto": KERNELS_AUTO, "dot4": KERNELS_DOT4, "mfma": KERNELS_MFMA, "both": KERNELS_BOTH}
 
 
 class Q8_1Struct(ctypes.Structure):

@@ -97,10 +97,10 @@ class HipWeight:
 
     @property
     def kernels(self) -> str:
-        """Kernel family the weight is laid out for: "dot4" or "mfma"."""
+        """Kernel family the weight is laid out for: "dot4", "mfma" or "both"."""
         f = ctypes.c_int()
         _lib.check(_lib.lib().rq_weight_kernels(self.handle, ctypes.byref(f)))
-        return "mfma" if f.value == _lib.KERNELS_MFMA else "dot4"
+        return {_lib.KERNELS_MFMA: "mfma", _lib.KERNELS_BOTH: "both"}.get(f.value, "dot4")
 
     def free(self) -> None:
         if self.handle:
@@ -182,7 +182,7 @@ class HipBackend:
         self.stream = stream
 
     def set_kernels(self, family: str) -> None:
-        """Kernel family ("auto", "dot4" or "mfma") for later uploads (rq_set_kernels)."""
+        """Kernel family ("auto", "dot4", "mfma" or "both") for later uploads (rq_set_kernels)."""
         if family not in _lib.KERNEL_FAMILIES:
             raise ValueError(f"unknown kernel family {family!r}")
         _lib.check(_lib.lib().rq_set_kernels(self.ctx, _lib.KERNEL_FAMILIES[family]))

@@ -259,7 +259,8 @@ struct rq_weight {
     int64_t rows = 0, cols = 0;
     void* base = nullptr;
     size_t bytes = 0;
-    bool mmq = false;  // 16-row tiles for the MFMA kernels; else tiled super-blocks
+    bool dot4 = false;  // holds the tiled super-blocks of the dot4 kernels
+    bool mmq = false;   // holds the 16-row tiles of the MFMA kernels (both: RQ_KERNELS_BOTH)
     // tiled super-blocks (dot4 kernels)
     RqTiled tiled{};
     size_t main_bytes = 0, tail_bytes = 0;
@@ -418,13 +419,23 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
     return RQ_OK;
 }
 
-// Whether weights a and b can share one matvec launch: the same type and
-// kernel family, or Q4_K and Q6_K in the dot4 layout (the mixed kernels).
-bool launch_compatible(const rq_weight* a, const rq_weight* b) {
-    if (a->mmq != b->mmq) return false;
+// Columns from which a weight holding both layouts runs its MFMA layout:
+// the measured crossover (Q4_K 14336 x 4096: dot4 8.08 / 10.92 us at 2 / 4
+// columns, MFMA 8.40 / 9.20).
+constexpr int64_t kMfmaMinCols = 4;
+
+// Whether a call over m activation columns runs w's MFMA layout.
+bool use_mmq(const rq_weight* w, int64_t m) { return w->mmq && (!w->dot4 || m >= kMfmaMinCols); }
+
+// Whether weights a and b can share one matvec launch over m columns: the
+// same type and kernel family, or Q4_K and Q6_K in the dot4 layout (the
+// mixed kernels).
+bool launch_compatible(const rq_weight* a, const rq_weight* b, int64_t m) {
+    const bool ma = use_mmq(a, m);
+    if (ma != use_mmq(b, m)) return false;
     if (a->type == b->type) return true;
     const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
-    return !a->mmq && ka && kb;
+    return !ma && ka && kb;
 }
 
 // Grows a Q8_1 scratch (codes q, scales d and s, capacity cap) to `values`
@@ -467,9 +478,9 @@ rq_status ensure_hscratch(rq_ctx* ctx, int64_t values) {
 // One launch can fuse gate, up and the activation when both weights are the
 // same type and shape in the dot4 layout, with whole 32-row blocks and tiles
 // of at most 32 rows (two or more super-blocks per row).
-bool glu_fusable(const rq_weight* gate, const rq_weight* up) {
-    return !gate->mmq && !up->mmq && gate->type == up->type && gate->rows == up->rows && gate->cols == up->cols &&
-           gate->rows % 32 == 0 && gate->tiled.R <= 32;
+bool glu_fusable(const rq_weight* gate, const rq_weight* up, int64_t m) {
+    return !use_mmq(gate, m) && !use_mmq(up, m) && gate->type == up->type && gate->rows == up->rows &&
+           gate->cols == up->cols && gate->rows % 32 == 0 && gate->tiled.R <= 32;
 }
 
 // LDS of an rq_glu workgroup: the staged columns, then g and u of its 32 rows.
@@ -915,8 +926,9 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     if (const char* v = getenv("RQ_KERNELS")) {
         if (!strcmp(v, "dot4")) ctx->kernels = RQ_KERNELS_DOT4;
         else if (!strcmp(v, "mfma")) ctx->kernels = RQ_KERNELS_MFMA;
+        else if (!strcmp(v, "both")) ctx->kernels = RQ_KERNELS_BOTH;
         else if (!strcmp(v, "auto") || !*v) ctx->kernels = RQ_KERNELS_AUTO;
-        else return bail(fail(RQ_ERR_INVALID, "rq_open: RQ_KERNELS=%s (auto, dot4 or mfma)", v));
+        else return bail(fail(RQ_ERR_INVALID, "rq_open: RQ_KERNELS=%s (auto, dot4, mfma or both)", v));
     }
     if (const char* v = getenv("RQ_MMQ_SBW")) ctx->mmq_sbw = atoi(v);
     if (const char* v = getenv("RQ_MMQ_TR")) ctx->mmq_tr = std::max(0, std::min(16, atoi(v)));
@@ -926,7 +938,7 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
 
 extern "C" rq_status rq_set_kernels(rq_ctx* ctx, int family) {
     if (!ctx) return fail(RQ_ERR_INVALID, "rq_set_kernels: null context");
-    if (family != RQ_KERNELS_AUTO && family != RQ_KERNELS_DOT4 && family != RQ_KERNELS_MFMA)
+    if (family != RQ_KERNELS_AUTO && family != RQ_KERNELS_DOT4 && family != RQ_KERNELS_MFMA && family != RQ_KERNELS_BOTH)
         return fail(RQ_ERR_INVALID, "rq_set_kernels: unknown family %d", family);
     ctx->kernels = family;
     return RQ_OK;
@@ -1018,23 +1030,30 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
     w->rows = rows;
     w->cols = cols;
     // AUTO lays weights out for the dot4 kernels, the faster family at one
-    // activation column (decode); MFMA is chosen explicitly (continuous batching).
-    w->mmq = ctx->kernels == RQ_KERNELS_MFMA && mmq_supported(fmt, cols);
-    size_t total = 0;
+    // activation column (decode); MFMA is chosen explicitly (continuous
+    // batching), or BOTH keeps both layouts and picks per call by the column
+    // count (twice the weight memory). Widths the MFMA kernels cannot stage
+    // take the dot4 layout.
+    const bool want_mmq = ctx->kernels == RQ_KERNELS_MFMA || ctx->kernels == RQ_KERNELS_BOTH;
+    w->mmq = want_mmq && mmq_supported(fmt, cols);
+    w->dot4 = !w->mmq || ctx->kernels == RQ_KERNELS_BOTH;
+    size_t dot4_bytes = 0, total = 0;
+    if (w->dot4) {
+        tile_geometry(rows, cols, w->tiled);
+        w->tiled.fmt = fmt;
+        const int64_t slots = (int64_t)w->tiled.T * w->tiled.R * w->tiled.S;
+        w->main_bytes = (size_t)(slots * rq_chunks(fmt) * 16);
+        w->tail_bytes = fmt == RQ_FMT_Q6_K ? (size_t)(slots * 2) : 0;
+        dot4_bytes = align_up(align_up(w->main_bytes, kPlaneAlign) + w->tail_bytes, kPlaneAlign);
+        total = dot4_bytes;
+    }
     if (w->mmq) {
         w->S2 = mmq_S2(cols);
         w->tiles = (int32_t)((rows + 15) / 16);
         w->code_bytes = (size_t)w->tiles * 16 * w->S2 * (fmt == RQ_FMT_Q8_0 ? 256 : fmt == RQ_FMT_Q6_K ? 192 : 128);
         w->hdr_bytes = (size_t)w->tiles * w->S2 * 256;
         if (fmt == RQ_FMT_Q6_K) w->hdr_bytes += (size_t)w->tiles * 16 * mmq_d_stride(w->S2) * 2;  // row scales d
-        total = align_up(align_up(w->code_bytes, kPlaneAlign) + w->hdr_bytes, kPlaneAlign);
-    } else {
-        tile_geometry(rows, cols, w->tiled);
-        w->tiled.fmt = fmt;
-        const int64_t slots = (int64_t)w->tiled.T * w->tiled.R * w->tiled.S;
-        w->main_bytes = (size_t)(slots * rq_chunks(fmt) * 16);
-        w->tail_bytes = fmt == RQ_FMT_Q6_K ? (size_t)(slots * 2) : 0;
-        total = align_up(align_up(w->main_bytes, kPlaneAlign) + w->tail_bytes, kPlaneAlign);
+        total += align_up(align_up(w->code_bytes, kPlaneAlign) + w->hdr_bytes, kPlaneAlign);
     }
     hipError_t e = hipMalloc(&w->base, total);
     if (e != hipSuccess) {
@@ -1042,12 +1061,13 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
         return hip_fail("hipMalloc", e);
     }
     w->bytes = total;
-    if (w->mmq) {
-        w->code = (const uint8_t*)w->base;
-        w->hdr = (const uint8_t*)w->base + align_up(w->code_bytes, kPlaneAlign);
-    } else {
+    if (w->dot4) {
         w->tiled.main = (const uint8_t*)w->base;
         w->tiled.tail = (const uint8_t*)w->base + align_up(w->main_bytes, kPlaneAlign);
+    }
+    if (w->mmq) {
+        w->code = (const uint8_t*)w->base + dot4_bytes;
+        w->hdr = w->code + align_up(w->code_bytes, kPlaneAlign);
     }
     // Padding (rows past the end, blocks past k) stays zero.
     e = hipMemsetAsync(w->base, 0, total, ctx->stream);
@@ -1091,7 +1111,8 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
             p.tiles = w->tiles;
             st = launch(ctx, ctx->mmq_repack[fmt], "rq_mmq_repack",
                         (uint64_t)((n * p.S2 + RQ_THREADS - 1) / RQ_THREADS), &p);
-        } else {
+        }
+        if (w->dot4 && st == RQ_OK) {
             RqRepackParams p;
             memset(&p, 0, sizeof p);
             p.raw = staging;
@@ -1139,7 +1160,7 @@ extern "C" rq_status rq_weight_shape(const rq_weight* w, int* type, int64_t* row
 
 extern "C" rq_status rq_weight_kernels(const rq_weight* w, int* family) {
     if (!w || !family) return fail(RQ_ERR_INVALID, "rq_weight_kernels: null argument");
-    *family = w->mmq ? RQ_KERNELS_MFMA : RQ_KERNELS_DOT4;
+    *family = w->mmq ? (w->dot4 ? RQ_KERNELS_BOTH : RQ_KERNELS_MFMA) : RQ_KERNELS_DOT4;
     return RQ_OK;
 }
 
@@ -1150,7 +1171,7 @@ extern "C" rq_status rq_weight_to_gguf(rq_ctx* ctx, const rq_weight* w, void* gg
     rq_status st = bind(ctx);
     if (st != RQ_OK) return st;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
-    if (w->mmq) {
+    if (!w->dot4) {
         std::vector<uint8_t> codep(w->code_bytes), hdrp(w->hdr_bytes);
         HIP_TRY(hipMemcpy(codep.data(), w->code, w->code_bytes, hipMemcpyDeviceToHost));
         HIP_TRY(hipMemcpy(hdrp.data(), w->hdr, w->hdr_bytes, hipMemcpyDeviceToHost));
@@ -1244,9 +1265,9 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
     for (int i = 0; i < count; i++) {
         if (!ws[i] || !outs[i]) return fail(RQ_ERR_INVALID, "matvec: null weight or output %d", i);
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matvec: output %d not 4-byte aligned", i);
-        if (ws[i]->mmq != ws[0]->mmq)
+        if (use_mmq(ws[i], m) != use_mmq(ws[0], m))
             return fail(RQ_ERR_SHAPE, "matvec: weights laid out for different kernel families in one launch");
-        if (!launch_compatible(ws[0], ws[i]))
+        if (!launch_compatible(ws[0], ws[i], m))
             return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
                         type_name(ws[i]->type));
         if (ws[i]->cols != ws[0]->cols)
@@ -1260,7 +1281,7 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if ((st = check_len("matmul out", out_lens[i], m * ws[i]->rows)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
-    if (ws[0]->mmq) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
+    if (use_mmq(ws[0], m)) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
     return matvec_launch(ctx, xq->qs, xq->d, nullptr, m, ws, outs, count);
 }
 
@@ -1320,11 +1341,11 @@ extern "C" rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, 
         int g = 1;
         while (g < RQ_MV_TARGETS && i + g < count) {
             bool ok = true;
-            for (int j = i; j < i + g; j++) ok = ok && launch_compatible(ws[j], ws[i + g]);
+            for (int j = i; j < i + g; j++) ok = ok && launch_compatible(ws[j], ws[i + g], m);
             if (!ok) break;
             g++;
         }
-        if (ws[i]->mmq)
+        if (use_mmq(ws[i], m))
             st = fused ? mmq_launch(ctx, nullptr, nullptr, x, m, ws + i, (void* const*)(outs + i), g, false)
                        : mmq_launch(ctx, ctx->sq, ctx->sd, nullptr, m, ws + i, (void* const*)(outs + i), g, false);
         else
@@ -1352,7 +1373,7 @@ extern "C" rq_status rq_block_dots(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, co
     if ((st = check_len("block_dots out", dots_len, m * w->rows * nb)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
-    if (w->mmq) {
+    if (use_mmq(w, m)) {
         void* out = dots;
         return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, &w, &out, 1, true);
     }
@@ -1378,7 +1399,7 @@ const char* act_name(int act) { return act == RQ_ACT_GELU_TANH ? "gelu_mul" : "s
 // One matvec group (same type and family) over Q8_1 activations.
 rq_status matvec_dispatch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, int64_t m, const rq_weight* const* ws,
                           float* const* outs, int count) {
-    if (ws[0]->mmq) return mmq_launch(ctx, xq, xd, nullptr, m, ws, (void* const*)outs, count, false);
+    if (use_mmq(ws[0], m)) return mmq_launch(ctx, xq, xd, nullptr, m, ws, (void* const*)outs, count, false);
     return matvec_launch(ctx, xq, xd, nullptr, m, ws, outs, count);
 }
 
@@ -1411,7 +1432,7 @@ rq_status glu_run(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* gate,
                   float* hf, float* u_buf, int8_t* hq, uint16_t* hd, uint16_t* hs) {
     const int64_t k = gate->cols, n = gate->rows;
     rq_status st;
-    if (glu_fusable(gate, up)) {
+    if (glu_fusable(gate, up, m)) {
         if (m == 1) return glu_launch(ctx, nullptr, nullptr, x, 1, gate, up, act, hf, hq, hd, hs);
         if ((st = ensure_scratch(ctx, m * k)) != RQ_OK) return st;
         RqQuantParams qp{x, ctx->sq, ctx->sd, ctx->ss, m * k / 32};
@@ -1531,7 +1552,7 @@ extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, i
     if ((st = check_len("glu_matmul out", out_len, m * n)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if (!out || !aligned(out, 16)) return fail(RQ_ERR_INVALID, "glu_matmul: out must be a 16-byte aligned pointer");
-    if (!glu_fusable(gate, up)) {
+    if (!glu_fusable(gate, up, m)) {
         if ((st = check_len("glu_matmul up", up_len, m * n)) != RQ_OK) return st;
         if (!up_scratch || !aligned(up_scratch, 16))
             return fail(RQ_ERR_INVALID, "glu_matmul: up scratch must be a 16-byte aligned pointer");
@@ -1553,7 +1574,7 @@ extern "C" rq_status rq_gated_ffn(rq_ctx* ctx, const float* x, int64_t x_len, in
                     (long long)n);
     if ((st = check_len("gated_ffn gate", gate_len, m * n)) != RQ_OK) return st;
     if ((st = check_len("matmul out", out_len, m * down->rows)) != RQ_OK) return st;
-    if (!glu_fusable(gate, up) && (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK) return st;
+    if (!glu_fusable(gate, up, m) && (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if (!out || !gate_buf || !aligned(out, 4) || !aligned(gate_buf, 16) || (up_buf && !aligned(up_buf, 16)))
         return fail(RQ_ERR_INVALID, "gated_ffn: null or misaligned buffer");

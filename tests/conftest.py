@@ -37,10 +37,11 @@ def gpu():
     b.close()
 
 
-@pytest.fixture(params=["dot4", "mfma"])
+@pytest.fixture(params=["dot4", "mfma", "both"])
 def gpuk(gpu, request):
-    """`gpu` with later uploads laid out for one kernel family (rq_set_kernels);
-    tests taking it run once per family."""
+    """`gpu` with later uploads laid out for one kernel family (rq_set_kernels;
+    "both" holds both layouts and picks per call); tests taking it run once
+    per family."""
     gpu.set_kernels(request.param)
     gpu.kernel_family = request.param
     yield gpu

@@ -196,3 +196,32 @@ def test_mmq_q6_k_extreme_codes(mfma, orc, m):
     orc.assert_close(f"extreme m={m}", orc.matvec_q8_1(t, w, n, k, qs, d, m), mfma.to_host(out, m * n), TOL_B)
     got = mfma.block_dots(xq, wg, m).cpu().numpy()
     assert np.array_equal(got, orc.block_dots(t, w, n, k, qs, m))
+
+
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
+def test_both_layouts_pick_by_column_count(gpu, orc, tname):
+    """RQ_KERNELS_BOTH: one weight in both layouts runs the dot4 kernels below
+    4 activation columns and the MFMA kernels from 4 up, bit for bit as the
+    single-layout weights; block dots and the GGUF round trip agree."""
+    t, n, k = MMQ_TYPES[tname], 70, 2048
+    w = make_weight(orc, t, n, k, 31, "random")
+    weights = {}
+    for fam in ("dot4", "mfma", "both"):
+        gpu.set_kernels(fam)
+        weights[fam] = upload(gpu, t, w, n, k)
+    gpu.set_kernels("auto")
+    assert [weights[f].kernels for f in ("dot4", "mfma", "both")] == ["dot4", "mfma", "both"]
+    assert np.array_equal(gpu.weight_to_gguf(weights["both"]), w)
+    assert weights["both"].device_bytes >= weights["dot4"].device_bytes + weights["mfma"].device_bytes
+    for m in (1, 2, 3, 4, 8, 17):
+        qs, d, s = orc.quantize_q8_1(orc.normal(50 + m, m * k, 0.0, 1.0), m, k)
+        xq = q8_1_to_device(gpu, qs, d, s)
+        outs = {}
+        for fam, wg in weights.items():
+            outs[fam] = gpu.alloc(m * n)
+            gpu.matvec(xq, wg, outs[fam], m)
+        want = "mfma" if m >= 4 else "dot4"
+        assert np.array_equal(gpu.to_host(outs["both"], m * n).view(np.uint32),
+                              gpu.to_host(outs[want], m * n).view(np.uint32)), f"m={m}"
+        assert np.array_equal(gpu.block_dots(xq, weights["both"], m).cpu().numpy(),
+                              orc.block_dots(t, w, n, k, qs, m))
