@@ -91,6 +91,8 @@ _SIGNATURES = {
     "rq_act_mul": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(Q8_1Struct)]),
     "rq_glu_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _int, _vp, _i64, _vp, _i64]),
     "rq_gated_ffn": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _int, _vp, _i64, _vp, _i64, _vp, _i64]),
+    "rq_gated_ffn_q8_1": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _vp, _int, _vp, _i64, _vp, _i64,
+                                 _vp, _i64]),
     "rq_weight_kernels": (_int, [_vp, ctypes.POINTER(_int)]),
     "rq_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "rq_gguf_close": (_int, [_vp]),

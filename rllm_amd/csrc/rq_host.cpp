@@ -1405,8 +1405,7 @@ rq_status matvec_dispatch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, int
 
 // Shared checks of rq_glu_matmul / rq_gated_ffn: gate and up of one shape, x
 // of m rows of their width.
-rq_status check_glu(const char* what, const float* x, int64_t x_len, int64_t m, const rq_weight* gate,
-                    const rq_weight* up, int act) {
+rq_status check_glu_shape(const char* what, int64_t m, const rq_weight* gate, const rq_weight* up, int act) {
     if (!gate || !up) return fail(RQ_ERR_INVALID, "%s: null weight", what);
     if (act != RQ_ACT_SILU && act != RQ_ACT_GELU_TANH) return fail(RQ_ERR_INVALID, "%s: unknown activation %d", what, act);
     if (gate->cols != up->cols)
@@ -1417,21 +1416,39 @@ rq_status check_glu(const char* what, const float* x, int64_t x_len, int64_t m, 
     if (gate->rows % 32 != 0)
         return fail(RQ_ERR_SHAPE, "%s: %lld FFN rows not a multiple of 32", what, (long long)gate->rows);
     if (m < 0) return fail(RQ_ERR_SHAPE, "%s: m = %lld", what, (long long)m);
+    return RQ_OK;
+}
+
+// The same and x: m rows of their width, f32 (16-byte aligned) or, when xq is
+// set, Q8_1.
+rq_status check_glu(const char* what, const float* x, int64_t x_len, const rq_q8_1* xq, int64_t m,
+                    const rq_weight* gate, const rq_weight* up, int act) {
+    rq_status st = check_glu_shape(what, m, gate, up, act);
+    if (st != RQ_OK) return st;
     char buf[64];
     snprintf(buf, sizeof buf, "%s x", what);
-    rq_status st = check_len(buf, x_len, m * gate->cols);
-    if (st != RQ_OK) return st;
+    if (xq) return check_q8_1(buf, xq, m * gate->cols);
+    if ((st = check_len(buf, x_len, m * gate->cols)) != RQ_OK) return st;
     if (m > 0 && (!x || !aligned(x, 16))) return fail(RQ_ERR_INVALID, "%s: x must be a 16-byte aligned pointer", what);
     return RQ_OK;
 }
 
-// h = act(x . gate) * (x . up) for x f32 [m, k]: into hf (f32, may be null)
-// and/or the Q8_1 (hq, hd, hs); u_buf (m * n floats) is used when the
-// launch cannot be fused.
-rq_status glu_run(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* gate, const rq_weight* up, int act,
-                  float* hf, float* u_buf, int8_t* hq, uint16_t* hd, uint16_t* hs) {
+// h = act(x . gate) * (x . up) for x f32 [m, k], or its Q8_1 xq when set:
+// into hf (f32, may be null) and/or the Q8_1 (hq, hd, hs); u_buf (m * n
+// floats) is used when the launch cannot be fused.
+rq_status glu_run(rq_ctx* ctx, const float* x, const rq_q8_1* xq, int64_t m, const rq_weight* gate,
+                  const rq_weight* up, int act, float* hf, float* u_buf, int8_t* hq, uint16_t* hd, uint16_t* hs) {
     const int64_t k = gate->cols, n = gate->rows;
     rq_status st;
+    if (xq) {
+        if (glu_fusable(gate, up, m)) return glu_launch(ctx, xq->qs, xq->d, nullptr, m, gate, up, act, hf, hq, hd, hs);
+        if (!hf || !u_buf) return fail(RQ_ERR_INVALID, "glu: unfused path needs the gate and up buffers");
+        const rq_weight* ws[2] = {gate, up};
+        float* outs[2] = {hf, u_buf};
+        const int64_t lens[2] = {m * n, m * n};
+        if ((st = rq_matvec_many(ctx, xq, m, ws, outs, lens, 2)) != RQ_OK) return st;
+        return act_mul_launch(ctx, act, hf, u_buf, m * n, hq, hd, hs);
+    }
     if (glu_fusable(gate, up, m)) {
         if (m == 1) return glu_launch(ctx, nullptr, nullptr, x, 1, gate, up, act, hf, hq, hd, hs);
         if ((st = ensure_scratch(ctx, m * k)) != RQ_OK) return st;
@@ -1546,7 +1563,7 @@ extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, i
                                    const rq_weight* up, int act, float* out, int64_t out_len, float* up_scratch,
                                    int64_t up_len) {
     if (!ctx) return fail(RQ_ERR_INVALID, "glu_matmul: null context");
-    rq_status st = check_glu("glu_matmul", x, x_len, m, gate, up, act);
+    rq_status st = check_glu("glu_matmul", x, x_len, nullptr, m, gate, up, act);
     if (st != RQ_OK) return st;
     const int64_t n = gate->rows;
     if ((st = check_len("glu_matmul out", out_len, m * n)) != RQ_OK) return st;
@@ -1558,30 +1575,52 @@ extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, i
             return fail(RQ_ERR_INVALID, "glu_matmul: up scratch must be a 16-byte aligned pointer");
     }
     if ((st = bind(ctx)) != RQ_OK) return st;
-    return glu_run(ctx, x, m, gate, up, act, out, up_scratch, nullptr, nullptr, nullptr);
+    return glu_run(ctx, x, nullptr, m, gate, up, act, out, up_scratch, nullptr, nullptr, nullptr);
 }
 
-extern "C" rq_status rq_gated_ffn(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* gate,
-                                  const rq_weight* up, const rq_weight* down, int act, float* out, int64_t out_len,
-                                  float* gate_buf, int64_t gate_len, float* up_buf, int64_t up_len) {
-    if (!ctx) return fail(RQ_ERR_INVALID, "gated_ffn: null context");
-    rq_status st = check_glu("gated_ffn", x, x_len, m, gate, up, act);
+namespace {
+
+// rq_gated_ffn over f32 x, or rq_gated_ffn_q8_1 over its Q8_1 xq (then x is
+// null and x_len unused).
+rq_status gated_ffn_run(rq_ctx* ctx, const char* what, const float* x, int64_t x_len, const rq_q8_1* xq, int64_t m,
+                        const rq_weight* gate, const rq_weight* up, const rq_weight* down, int act, float* out,
+                        int64_t out_len, float* gate_buf, int64_t gate_len, float* up_buf, int64_t up_len) {
+    if (!ctx) return fail(RQ_ERR_INVALID, "%s: null context", what);
+    rq_status st = check_glu(what, x, x_len, xq, m, gate, up, act);
     if (st != RQ_OK) return st;
-    if (!down) return fail(RQ_ERR_INVALID, "gated_ffn: null down weight");
+    if (!down) return fail(RQ_ERR_INVALID, "%s: null down weight", what);
     const int64_t n = gate->rows;
     if (down->cols != n)
-        return fail(RQ_ERR_SHAPE, "gated_ffn: down takes %lld columns, the FFN has %lld", (long long)down->cols,
+        return fail(RQ_ERR_SHAPE, "%s: down takes %lld columns, the FFN has %lld", what, (long long)down->cols,
                     (long long)n);
     if ((st = check_len("gated_ffn gate", gate_len, m * n)) != RQ_OK) return st;
     if ((st = check_len("matmul out", out_len, m * down->rows)) != RQ_OK) return st;
     if (!glu_fusable(gate, up, m) && (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if (!out || !gate_buf || !aligned(out, 4) || !aligned(gate_buf, 16) || (up_buf && !aligned(up_buf, 16)))
-        return fail(RQ_ERR_INVALID, "gated_ffn: null or misaligned buffer");
+        return fail(RQ_ERR_INVALID, "%s: null or misaligned buffer", what);
     if ((st = bind(ctx)) != RQ_OK) return st;
     // The product goes to the down projection as Q8_1, written by the launch
     // that computes it (as the reference's glu_mmq int8 copy, backend.rs:989-1093).
     if ((st = ensure_hscratch(ctx, m * n)) != RQ_OK) return st;
-    if ((st = glu_run(ctx, x, m, gate, up, act, gate_buf, up_buf, ctx->hq, ctx->hd, ctx->hs)) != RQ_OK) return st;
+    if ((st = glu_run(ctx, x, xq, m, gate, up, act, gate_buf, up_buf, ctx->hq, ctx->hd, ctx->hs)) != RQ_OK) return st;
     return matvec_dispatch(ctx, ctx->hq, ctx->hd, m, &down, &out, 1);
+}
+
+}  // namespace
+
+extern "C" rq_status rq_gated_ffn(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* gate,
+                                  const rq_weight* up, const rq_weight* down, int act, float* out, int64_t out_len,
+                                  float* gate_buf, int64_t gate_len, float* up_buf, int64_t up_len) {
+    return gated_ffn_run(ctx, "gated_ffn", x, x_len, nullptr, m, gate, up, down, act, out, out_len, gate_buf, gate_len,
+                         up_buf, up_len);
+}
+
+extern "C" rq_status rq_gated_ffn_q8_1(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* gate,
+                                       const rq_weight* up, const rq_weight* down, int act, float* out,
+                                       int64_t out_len, float* gate_buf, int64_t gate_len, float* up_buf,
+                                       int64_t up_len) {
+    if (!xq) return fail(RQ_ERR_INVALID, "gated_ffn: null Q8_1 input");
+    return gated_ffn_run(ctx, "gated_ffn", nullptr, 0, xq, m, gate, up, down, act, out, out_len, gate_buf, gate_len,
+                         up_buf, up_len);
 }

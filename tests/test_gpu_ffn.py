@@ -175,3 +175,32 @@ def test_gated_ffn_errors(gpu, orc):
         gpu.gated_ffn(gpu.alloc(k), w, w, dn, Activation.SILU, gpu.alloc(k), gpu.alloc(n), gpu.alloc(n), 1)
     with pytest.raises(ShapeError, match="gated_ffn x: buffer has 100 elements, need 256"):
         gpu.gated_ffn(gpu.alloc(100), w, w, dn, Activation.SILU, gpu.alloc(k), gpu.alloc(n), gpu.alloc(n), 1)
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_gated_ffn_q8_1_input(gpuk, orc, tname, m):
+    """rq_gated_ffn_q8_1 on the Q8_1 that rq_add_rms_norm emits (the
+    reference's prequant path): bit-identical to rq_gated_ffn on the norm's
+    f32 output, in every kernel family."""
+    t, d, f = TYPES[tname], 1024, 2048
+    gw = orc.random_weight(0xC0 + m, t, f, d)
+    uw = orc.random_weight(0xC1 + m, t, f, d)
+    dw = orc.random_weight(0xC2 + m, t, d, f)
+    g, u, dn = upload(gpuk, t, gw, f, d), upload(gpuk, t, uw, f, d), upload(gpuk, t, dw, d, f)
+    resid = gpuk.from_host(orc.normal(0xC3 + m, m * d, 0.0, 1.0))
+    delta = gpuk.from_host(orc.normal(0xC4 + m, m * d, 0.0, 1.0))
+    nw = gpuk.from_host(orc.uniform(0xC5, d) + 1.0)
+    normed = gpuk.alloc(m * d)
+    xq = Q8_1.empty(m * d, gpuk.device)
+    gpuk.add_rms_norm(resid, delta, nw, normed, m, d, 1e-6, qout=xq)
+    outs = []
+    for use_q8 in (False, True):
+        out, gb, ub = gpuk.alloc(m * d), gpuk.alloc(m * f), gpuk.alloc(m * f)
+        if use_q8:
+            gpuk.gated_ffn_q8_1(xq, g, u, dn, Activation.SILU, out, gb, ub, m)
+        else:
+            gpuk.gated_ffn(normed, g, u, dn, Activation.SILU, out, gb, ub, m)
+        outs.append((gpuk.to_host(out, m * d), gpuk.to_host(gb, m * f)))
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32)), "h"
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32)), "out"
