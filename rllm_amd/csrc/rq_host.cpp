@@ -234,10 +234,11 @@ struct rq_ctx {
     // 2, 4, 8) and super-blocks per wave (sbw = 2, 4, 8); null where a
     // format has none.
     hipModule_t mmq_mod = nullptr;
-    hipFunction_t mmq[RQ_NUM_FMTS][3][3] = {};
-    hipFunction_t mmqf[RQ_NUM_FMTS][3] = {};
+    // (index RQ_NUM_FMTS: the mixed Q4_K / Q6_K launches, no block dots)
+    hipFunction_t mmq[RQ_NUM_FMTS + 1][3][3] = {};
+    hipFunction_t mmqf[RQ_NUM_FMTS + 1][3] = {};
     hipFunction_t mmqd[RQ_NUM_FMTS][3][3] = {};
-    hipFunction_t mmqg[RQ_NUM_FMTS][2][3] = {};  // 8 x G columns, G = 2, 4
+    hipFunction_t mmqg[RQ_NUM_FMTS + 1][2][3] = {};  // 8 x G columns, G = 2, 4
     hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
@@ -428,14 +429,14 @@ constexpr int64_t kMfmaMinCols = 4;
 bool use_mmq(const rq_weight* w, int64_t m) { return w->mmq && (!w->dot4 || m >= kMfmaMinCols); }
 
 // Whether weights a and b can share one matvec launch over m columns: the
-// same type and kernel family, or Q4_K and Q6_K in the dot4 layout (the
-// mixed kernels).
+// same type and kernel family, or Q4_K and Q6_K in one family (the mixed
+// kernels).
 bool launch_compatible(const rq_weight* a, const rq_weight* b, int64_t m) {
     const bool ma = use_mmq(a, m);
     if (ma != use_mmq(b, m)) return false;
     if (a->type == b->type) return true;
     const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
-    return !ma && ka && kb;
+    return ka && kb;
 }
 
 // Grows a Q8_1 scratch (codes q, scales d and s, capacity cap) to `values`
@@ -547,7 +548,7 @@ int mmq_mp_index(int mp) { return mp == 1 ? 0 : mp == 4 ? 1 : 2; }
 int mmq_sbw_index(int sbw) { return sbw == 2 ? 0 : sbw == 4 ? 1 : 2; }
 // Most super-blocks per wave the format's kernels exist for (Q8_0 keeps 16 B
 // of codes per window in registers, Q6_K 12, so they stop at 4).
-int mmq_sbw_max(int fmt) { return fmt == RQ_FMT_Q8_0 || fmt == RQ_FMT_Q6_K ? 4 : 8; }
+int mmq_sbw_max(int fmt) { return fmt == RQ_FMT_Q8_0 || fmt == RQ_FMT_Q6_K || fmt == RQ_FMT_MIX_K ? 4 : 8; }
 int mmq_planes(int fmt) { return fmt == RQ_FMT_Q8_0 || fmt == RQ_FMT_Q6_K ? 1 : 2; }
 int mmq_S2(int64_t cols) { return (int)((cols + 511) / 512 * 2); }
 // f16 row scales d per Q6_K row (super-blocks, padded to a multiple of 8).
@@ -571,10 +572,14 @@ struct MmqPlan {
     int kxp, pl_off, part_off, lds;
 };
 
+// Kernel table index of a format (RQ_FMT_MIX_K: the mixed Q4_K / Q6_K kernels).
+int mmq_fi(int fmt) { return fmt == RQ_FMT_MIX_K ? RQ_NUM_FMTS : fmt; }
+
 hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int g, int sbw, bool f32_in, bool dots) {
-    const int si = mmq_sbw_index(sbw), mi = mmq_mp_index(mp);
-    if (g > 1) return ctx->mmqg[fmt][g == 2 ? 0 : 1][si];
-    return f32_in ? ctx->mmqf[fmt][si] : dots ? ctx->mmqd[fmt][mi][si] : ctx->mmq[fmt][mi][si];
+    const int si = mmq_sbw_index(sbw), mi = mmq_mp_index(mp), fi = mmq_fi(fmt);
+    if (g > 1) return ctx->mmqg[fi][g == 2 ? 0 : 1][si];
+    if (dots) return fmt == RQ_FMT_MIX_K ? nullptr : ctx->mmqd[fmt][mi][si];
+    return f32_in ? ctx->mmqf[fi][si] : ctx->mmq[fi][mi][si];
 }
 
 void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
@@ -679,7 +684,9 @@ void mmq_cols(int nc, int& mp, int& g) {
 // `outs` are then int32 arrays).
 rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
                      const rq_weight* const* ws, void* const* outs, int count, bool dots) {
-    const int fmt = ws[0]->fmt;
+    int fmt = ws[0]->fmt;
+    for (int i = 1; i < count; i++)
+        if (ws[i]->fmt != fmt) fmt = RQ_FMT_MIX_K;  // Q4_K with Q6_K (launch_compatible)
     const int64_t k = ws[0]->cols, U = k / 32, nb = fmt == RQ_FMT_Q6_K ? k / 16 : U;  // nb: block dots per row
     const int S2 = ws[0]->S2;
     int64_t tiles = 0;
@@ -712,6 +719,7 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
             p.t[i].n = (int32_t)w->rows;
             p.t[i].tiles = w->tiles;
             p.t[i].wg_start = (int32_t)wgs;
+            p.t[i].fmt = w->fmt;
             wgs += (w->tiles + P.tr - 1) / P.tr;
         }
         if (xf) {
@@ -919,6 +927,19 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
                 snprintf(name, sizeof name, "rq_mmqd_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
                 st = getm(ctx->mmq_mod, &ctx->mmqd[f][mi][si], name);
             }
+        }
+    }
+    for (int si = 0; si < 2 && st == RQ_OK; si++) {  // mixed Q4_K / Q6_K: sbw 2 and 4
+        const int fi = RQ_NUM_FMTS;
+        snprintf(name, sizeof name, "rq_mmqf_q4_k_q6_k_%d", kMmqSbw[si]);
+        st = getm(ctx->mmq_mod, &ctx->mmqf[fi][si], name);
+        for (int gi = 0; gi < 2 && st == RQ_OK; gi++) {
+            snprintf(name, sizeof name, "rq_mmq_q4_k_q6_k_8x%d_%d", 2 << gi, kMmqSbw[si]);
+            st = getm(ctx->mmq_mod, &ctx->mmqg[fi][gi][si], name);
+        }
+        for (int mi = 0; mi < 3 && st == RQ_OK; mi++) {
+            snprintf(name, sizeof name, "rq_mmq_q4_k_q6_k_%d_%d", kMmqMp[mi], kMmqSbw[si]);
+            st = getm(ctx->mmq_mod, &ctx->mmq[fi][mi][si], name);
         }
     }
     if (st != RQ_OK) return bail(st);

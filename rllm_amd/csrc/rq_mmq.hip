@@ -5,7 +5,7 @@
 //   rq_mmq_<fmt>_8x<g>_<sbw> up to 8 g columns (g = 2, 4 groups of 8, weights read once)
 //   rq_mmqf_<fmt>_<sbw>      one f32 activation column, quantized while staging
 //   rq_mmqd_<fmt>_<mp>_<sbw> the int32 block dots of the same MFMA path (debug)
-//   (fmt: q4_0, q8_0, q4_k, q6_k)
+//   (fmt: q4_0, q8_0, q4_k, q6_k, and q4_k_q6_k for launches mixing the two)
 //   rq_mmq_repack_<fmt>      GGUF rows -> 16-row tiles (upload)
 //
 // Work split. A wave owns one tile (16 weight rows) and one k-part of sbw
@@ -256,8 +256,8 @@ __device__ __forceinline__ RqMmqTarget pick_target(const RqMmqParams& P, int ti)
     RQ_PICK(n)
     RQ_PICK(tiles)
     RQ_PICK(wg_start)
+    RQ_PICK(fmt)
 #undef RQ_PICK
-    r.pad = 0;
     return r;
 }
 
@@ -800,13 +800,27 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     mmq_reduce<MP, G, NACC>(P, T);
 }
 
-// Kernel bodies by format.
+// Kernel bodies by format. RQ_FMT_MIX_K: launches whose targets mix Q4_K
+// and Q6_K weights of one width (q, k and v of a Q4_K_M layer); a workgroup
+// serves one target, so it branches once, on that target's format, into its
+// body (staging included; the host sizes LDS for Q4_K's two planes).
 template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1>
 __device__ __forceinline__ void mmq_run(const RqMmqParams& P) {
-    if constexpr (FMT == RQ_FMT_Q6_K)
+    if constexpr (FMT == RQ_FMT_Q6_K) {
         mmq6_body<MP, SBW, F32IN, DOTS, G>(P);
-    else
+    } else if constexpr (FMT == RQ_FMT_MIX_K) {
+        const int blk = blockIdx.x;
+        int ti = 0;
+        if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
+        if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+        const int fmt = pick_target(P, ti).fmt;  // workgroup-uniform
+        if (fmt == RQ_FMT_Q6_K)
+            mmq6_body<MP, SBW, F32IN, DOTS, G>(P);
+        else
+            mmq_body<RQ_FMT_Q4_K, MP, SBW, F32IN, DOTS, G>(P);
+    } else {
         mmq_body<FMT, MP, SBW, F32IN, DOTS, G>(P);
+    }
 }
 
 #define RQ_MMQ(NAME, FMT, MP, SBW)                                                                  \
@@ -842,6 +856,22 @@ RQ_MMQ_SET(q4_k, RQ_FMT_Q4_K, 8)
 // Q6_K holds 48 B of codes per lane per super-block: sbw = 8 would need 96 registers of them.
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 2)
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 4)
+// Mixed Q4_K / Q6_K launches (no block-dot variants: those run per weight).
+#define RQ_MMQ_MIX(MP, SBW)                                                                          \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_q4_k_q6_k_##MP##_##SBW(RqMmqParams p) { \
+        mmq_run<RQ_FMT_MIX_K, MP, SBW, false, false>(p);                                             \
+    }
+#define RQ_MMQ_MIX_SET(SBW)                                                                          \
+    RQ_MMQ_MIX(1, SBW)                                                                               \
+    RQ_MMQ_MIX(4, SBW)                                                                               \
+    RQ_MMQ_MIX(8, SBW)                                                                               \
+    RQ_MMQ_G(q4_k_q6_k, RQ_FMT_MIX_K, 2, SBW)                                                        \
+    RQ_MMQ_G(q4_k_q6_k, RQ_FMT_MIX_K, 4, SBW)                                                        \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqf_q4_k_q6_k_##SBW(RqMmqParams p) {        \
+        mmq_run<RQ_FMT_MIX_K, 1, SBW, true, false>(p);                                               \
+    }
+RQ_MMQ_MIX_SET(2)
+RQ_MMQ_MIX_SET(4)
 
 // ---------------------------------------------------------------------------
 // Repack GGUF rows into 16-row tiles: one thread per (row, super-block) of

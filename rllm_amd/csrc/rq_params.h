@@ -170,7 +170,7 @@ struct RqMmqTarget {
     int32_t n;            // rows
     int32_t tiles;        // ceil(n / 16)
     int32_t wg_start;     // first workgroup of this target
-    int32_t pad;
+    int32_t fmt;          // RQ_FMT_* (read by the mixed Q4_K / Q6_K kernels)
 };
 
 struct RqMmqParams {

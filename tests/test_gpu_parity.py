@@ -298,14 +298,24 @@ def test_matmul_many_grouping(gpuk, orc, m):
         orc.assert_close(f"many type {t} rows {n}", orc.matvec_q8_1(t, w, n, k, qs, d, m), gpuk.to_host(o, m * n), TOL_B)
 
 
+@pytest.mark.parametrize("family", ["dot4", "mfma"])
 @pytest.mark.parametrize("k", [1024, 4096, 14336, 20480])
-@pytest.mark.parametrize("m", [1, 3])
-def test_mixed_q4k_q6k_launch(gpu, orc, k, m):
-    """q, k (Q4_K) and v (Q6_K) of a Q4_K_M layer share one launch (rq_mvxm /
-    rq_mvfm): each output is bit-identical to its own single-weight launch."""
+@pytest.mark.parametrize("m", [1, 3, 8, 20])
+def test_mixed_q4k_q6k_launch(gpu, orc, family, k, m):
+    """q, k (Q4_K) and v (Q6_K) of a Q4_K_M layer share one launch (dot4:
+    rq_mvxm / rq_mvfm; MFMA: rq_mmq_q4_k_q6_k_*, a workgroup running its
+    target's format): each output is bit-identical to its own single-weight
+    launch."""
+    if family == "mfma" and k > 16384:
+        pytest.skip("Q6_K over 16384 columns runs the dot4 kernels")
     spec = [(12, 64), (12, 16), (14, 16)] if k <= 4096 else [(12, 12), (14, 5), (12, 7)]
     ws = [make_weight(orc, t, n, k, 700 + i, "random") for i, (t, n) in enumerate(spec)]
-    wgs = [upload(gpu, t, w, n, k) for (t, n), w in zip(spec, ws)]
+    gpu.set_kernels(family)
+    try:
+        wgs = [upload(gpu, t, w, n, k) for (t, n), w in zip(spec, ws)]
+    finally:
+        gpu.set_kernels("auto")
+    assert all(wg.kernels == family for wg in wgs)
     x = gpu.from_host(_x(orc, 701, m, k))
     together = [gpu.alloc(m * n) for _, n in spec]
     gpu.matmul_many(x, wgs, together, m)
