@@ -239,6 +239,9 @@ struct rq_ctx {
     hipFunction_t mmqf[RQ_NUM_FMTS + 1][3] = {};
     hipFunction_t mmqd[RQ_NUM_FMTS][3][3] = {};
     hipFunction_t mmqg[RQ_NUM_FMTS + 1][2][3] = {};  // 8 x G columns, G = 2, 4
+    // fused gate/up + activation (sbw 4): column classes 1, 4, 8, 8x2, 8x4; f32 x
+    hipFunction_t mmqglu[RQ_NUM_FMTS][5] = {};
+    hipFunction_t mmqgluf[RQ_NUM_FMTS] = {};
     hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
@@ -748,6 +751,88 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     return RQ_OK;
 }
 
+// Fused gate/up + activation over the MFMA layout (rq_mmqglu_*): gate and up
+// of one type and shape whose two weights' k-parts (4 super-blocks per wave)
+// of two 16-row tiles fit one workgroup (rows of at most 16 super-blocks),
+// n % 32 == 0 (a workgroup's 32 rows are one Q8_1 block of h per column).
+bool glu_mmq_ok(const rq_weight* gate, const rq_weight* up, int64_t m) {
+    return use_mmq(gate, m) && use_mmq(up, m) && gate->type == up->type && gate->rows == up->rows &&
+           gate->cols == up->cols && gate->rows % 32 == 0 && gate->S2 <= 16;
+}
+
+// h = act(x . gate) * (x . up) into hf (may be null) and the Q8_1 (hq, hd,
+// hs; may be null) over Q8_1 x (xq, xd) or one f32 column xf, in launches of
+// <= 32 columns. Workgroup: 2 tiles x ks k-parts of gate, then of up.
+rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const float* xf, int64_t m,
+                         const rq_weight* gate, const rq_weight* up, int act, float* hf, int8_t* hq, uint16_t* hd,
+                         uint16_t* hs) {
+    const int fmt = gate->fmt, S2 = gate->S2;
+    const int64_t k = gate->cols, n = gate->rows, U = k / 32;
+    auto plan = [&](int nc, MmqPlan& L, int& h_off) {
+        mmq_cols(nc, L.mp, L.g);
+        L.sbw = 4;
+        L.ks = (S2 + 3) / 4;
+        L.tr = 2;
+        mmq_layout(fmt, S2, false, L);
+        h_off = L.part_off + 2 * L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4;  // both weights' partials
+        L.lds = h_off + L.g * L.mp * 32 * 4;
+    };
+    const int max_cols = xf ? 1 : kMmqMaxCols;
+    int64_t ngroups = (m + max_cols - 1) / max_cols;
+    for (;;) {
+        MmqPlan L;
+        int h_off;
+        plan((int)((m + ngroups - 1) / ngroups), L, h_off);
+        if (L.lds <= ctx->lds_wide) break;
+        if (m / ngroups <= 1) return fail(RQ_ERR_SHAPE, "glu: %lld columns too wide to stage", (long long)k);
+        ngroups++;
+    }
+    for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
+        const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
+        MmqPlan L;
+        int h_off;
+        plan(nc, L, h_off);
+        RqMmqParams p;
+        memset(&p, 0, sizeof p);
+        const rq_weight* ws[2] = {gate, up};
+        for (int i = 0; i < 2; i++) {
+            p.t[i].code = ws[i]->code;
+            p.t[i].hdr = ws[i]->hdr;
+            p.t[i].n = (int32_t)n;
+            p.t[i].tiles = ws[i]->tiles;
+            p.t[i].fmt = fmt;
+        }
+        if (xf) {
+            p.xf = xf + g0 * k;
+        } else {
+            p.xq = xq + g0 * k;
+            p.xd = xd + g0 * U;
+        }
+        p.count = 2;
+        p.m = nc;
+        p.k = (int32_t)k;
+        p.S2 = S2;
+        p.ks = L.ks;
+        p.tr = L.tr;
+        p.kxp = L.kxp;
+        p.pl_off = L.pl_off;
+        p.part_off = L.part_off;
+        p.h_off = h_off;
+        p.hf = hf ? hf + g0 * n : nullptr;
+        p.hq = hq ? hq + g0 * n : nullptr;
+        p.hd = hq ? hd + g0 * n / 32 : nullptr;
+        p.hs = hq ? hs + g0 * n / 32 : nullptr;
+        p.act = act;
+        const int cls = L.g > 1 ? (L.g == 2 ? 3 : 4) : mmq_mp_index(L.mp);
+        hipFunction_t f = xf ? ctx->mmqgluf[fmt] : ctx->mmqglu[fmt][cls];
+        rq_status st = launch(ctx, f, xf ? "rq_mmqgluf" : "rq_mmqglu", (uint64_t)(gate->tiles / 2), &p,
+                              (unsigned)L.lds, (unsigned)(64 * 2 * L.ks * L.tr));
+        if (st != RQ_OK) return st;
+        g0 += nc;
+    }
+    return RQ_OK;
+}
+
 // 16-row tiles back to GGUF rows (host side of rq_weight_to_gguf).
 void mmq_to_gguf(const rq_weight* w, const uint8_t* code, const uint8_t* hdr, uint8_t* out) {
     const int fmt = w->fmt, S2 = w->S2;
@@ -928,6 +1013,15 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
                 st = getm(ctx->mmq_mod, &ctx->mmqd[f][mi][si], name);
             }
         }
+    }
+    for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
+        static const char* const kGluClass[5] = {"1", "4", "8", "8x2", "8x4"};
+        for (int c = 0; c < 5 && st == RQ_OK; c++) {
+            snprintf(name, sizeof name, "rq_mmqglu_%s_%s", kFmtSuffix[f], kGluClass[c]);
+            st = getm(ctx->mmq_mod, &ctx->mmqglu[f][c], name);
+        }
+        snprintf(name, sizeof name, "rq_mmqgluf_%s", kFmtSuffix[f]);
+        if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmqgluf[f], name);
     }
     for (int si = 0; si < 2 && st == RQ_OK; si++) {  // mixed Q4_K / Q6_K: sbw 2 and 4
         const int fi = RQ_NUM_FMTS;
@@ -1461,6 +1555,16 @@ rq_status glu_run(rq_ctx* ctx, const float* x, const rq_q8_1* xq, int64_t m, con
                   const rq_weight* up, int act, float* hf, float* u_buf, int8_t* hq, uint16_t* hd, uint16_t* hs) {
     const int64_t k = gate->cols, n = gate->rows;
     rq_status st;
+    if (glu_mmq_ok(gate, up, m)) {
+        if (xq) return mmq_glu_launch(ctx, xq->qs, xq->d, nullptr, m, gate, up, act, hf, hq, hd, hs);
+        if (m == 1) return mmq_glu_launch(ctx, nullptr, nullptr, x, 1, gate, up, act, hf, hq, hd, hs);
+        if ((st = ensure_scratch(ctx, m * k)) != RQ_OK) return st;
+        RqQuantParams qp{x, ctx->sq, ctx->sd, ctx->ss, m * k / 32};
+        if ((st = launch(ctx, ctx->quant, "rq_quantize_q8_1",
+                         (uint64_t)((qp.nblocks * 8 + RQ_THREADS - 1) / RQ_THREADS), &qp)) != RQ_OK)
+            return st;
+        return mmq_glu_launch(ctx, ctx->sq, ctx->sd, nullptr, m, gate, up, act, hf, hq, hd, hs);
+    }
     if (xq) {
         if (glu_fusable(gate, up, m)) return glu_launch(ctx, xq->qs, xq->d, nullptr, m, gate, up, act, hf, hq, hd, hs);
         if (!hf || !u_buf) return fail(RQ_ERR_INVALID, "glu: unfused path needs the gate and up buffers");
@@ -1590,7 +1694,7 @@ extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, i
     if ((st = check_len("glu_matmul out", out_len, m * n)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if (!out || !aligned(out, 16)) return fail(RQ_ERR_INVALID, "glu_matmul: out must be a 16-byte aligned pointer");
-    if (!glu_fusable(gate, up, m)) {
+    if (!glu_fusable(gate, up, m) && !glu_mmq_ok(gate, up, m)) {
         if ((st = check_len("glu_matmul up", up_len, m * n)) != RQ_OK) return st;
         if (!up_scratch || !aligned(up_scratch, 16))
             return fail(RQ_ERR_INVALID, "glu_matmul: up scratch must be a 16-byte aligned pointer");
@@ -1616,7 +1720,9 @@ rq_status gated_ffn_run(rq_ctx* ctx, const char* what, const float* x, int64_t x
                     (long long)n);
     if ((st = check_len("gated_ffn gate", gate_len, m * n)) != RQ_OK) return st;
     if ((st = check_len("matmul out", out_len, m * down->rows)) != RQ_OK) return st;
-    if (!glu_fusable(gate, up, m) && (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK) return st;
+    if (!glu_fusable(gate, up, m) && !glu_mmq_ok(gate, up, m) &&
+        (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK)
+        return st;
     if (m == 0) return RQ_OK;
     if (!out || !gate_buf || !aligned(out, 4) || !aligned(gate_buf, 16) || (up_buf && !aligned(up_buf, 16)))
         return fail(RQ_ERR_INVALID, "%s: null or misaligned buffer", what);

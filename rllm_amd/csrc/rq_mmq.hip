@@ -6,6 +6,7 @@
 //   rq_mmqf_<fmt>_<sbw>      one f32 activation column, quantized while staging
 //   rq_mmqd_<fmt>_<mp>_<sbw> the int32 block dots of the same MFMA path (debug)
 //   (fmt: q4_0, q8_0, q4_k, q6_k, and q4_k_q6_k for launches mixing the two)
+//   rq_mmqglu_<fmt>_<cls>    gate and up with act(g) * u and its Q8_1 (rq_mmqgluf_<fmt>: f32 x)
 //   rq_mmq_repack_<fmt>      GGUF rows -> 16-row tiles (upload)
 //
 // Work split. A wave owns one tile (16 weight rows) and one k-part of sbw
@@ -301,6 +302,15 @@ __device__ __forceinline__ void mmq_part_store(const RqMmqParams& P, float (&y)[
     for (int e = 0; e < NACC; e++) part[(slot * 64 + lane) * NACC + e] = y[e];
 }
 
+// Partial sum of activation a, tile row nn, left by wave slot w (mmq_part_store).
+template <int MP>
+__device__ __forceinline__ float part_at(const float* part, int w, int a, int nn) {
+    if (MP == 1) return part[w * 64 + nn];
+    if (MP == 2) return part[w * 64 + 16 * (2 * a) + nn];
+    if (MP == 4) return part[w * 64 + 16 * a + nn];
+    return part[(w * 64 + 16 * (a >> 1) + nn) * 2 + (a & 1)];
+}
+
 // The tile's sums, in a fixed order: the k-parts' partial sums in LDS.
 template <int MP, int G, int NACC>
 __device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarget& T) {
@@ -315,19 +325,46 @@ __device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarg
         const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn;
         if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
         float s = 0.f;
-        for (int q = 0; q < ks; q++) {
-            const int w = (tl2 * ks + q) * G + gi;
-            if (MP == 1) {
-                s += part[w * 64 + nn];
-            } else if (MP == 2) {
-                s += part[w * 64 + 16 * (2 * a) + nn];
-            } else if (MP == 4) {
-                s += part[w * 64 + 16 * a + nn];
-            } else {
-                s += part[(w * 64 + 16 * (a >> 1) + nn) * 2 + (a & 1)];
-            }
-        }
+        for (int q = 0; q < ks; q++) s += part_at<MP>(part, (tl2 * ks + q) * G + gi, a, nn);
         gmem(out)[(int64_t)ag * T.n + row] = s;
+    }
+}
+
+// rq_mmqglu_*: the workgroup's two tiles of gate (waves 0 .. ks tr - 1) and
+// of up (the next ks tr) meet as h = act(g) * u (act_apply, as rq_act_mul),
+// written as f32 (hf, when set) and, per column, as the Q8_1 block of the 32
+// rows (q8_emit4, as rq_quantize_q8_1).
+template <int MP, int G, int NACC>
+__device__ __forceinline__ void mmq_reduce_glu(const RqMmqParams& P, const RqMmqTarget& T) {
+    constexpr int NCOL = G * MP;
+    const int threads = blockDim.x, tid = threadIdx.x;
+    const int blk = blockIdx.x, ks = P.ks, kt = P.ks * P.tr;
+    const float* part = (const float*)(mmq_lds + P.part_off);
+    float* hl = (float*)(mmq_lds + P.h_off);  // [NCOL][32]
+    __syncthreads();
+    for (int it = tid; it < P.tr * NCOL * 16; it += threads) {
+        const int tl2 = it / (NCOL * 16), ag = (it >> 4) % NCOL, nn = it & 15;
+        const int gi = ag / MP, a = ag % MP;
+        float g = 0.f, u = 0.f;
+        for (int q = 0; q < ks; q++) {
+            g += part_at<MP>(part, (tl2 * ks + q) * G + gi, a, nn);
+            u += part_at<MP>(part, (kt + tl2 * ks + q) * G + gi, a, nn);
+        }
+        const float h = act_apply(P.act, g) * u;
+        const int row = (blk * P.tr + tl2) * 16 + nn;
+        if (P.hf && ag < P.m) gmem(P.hf)[(int64_t)ag * T.n + row] = h;
+        hl[ag * 32 + tl2 * 16 + nn] = h;
+    }
+    if (!P.hq) return;  // uniform
+    __syncthreads();
+    for (int base = 0; base < NCOL * 8; base += threads) {  // uniform trip count: whole 8-lane groups
+        const int t = base + tid;
+        const bool in = t < NCOL * 8;
+        const int ag = in ? t >> 3 : 0, f4 = t & 7;
+        float h[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) h[j] = hl[ag * 32 + 4 * f4 + j];
+        q8_emit4(h, ((int64_t)ag * T.n + blk * 32) / 4 + f4, in && ag < P.m, P.hq, P.hd, P.hs);
     }
 }
 
@@ -337,7 +374,7 @@ __device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarg
 // G > 1 (mp = 8): the launch's columns come in G groups of 8 that are staged
 // and computed one after another through the same LDS, against weights loaded
 // once into registers.
-template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1>
+template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
 __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr bool NIB = MF<FMT>::NIB;
     constexpr int PS = 16 / MP;                // D rows (slots) per activation
@@ -355,14 +392,19 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     const int g = lane >> 4, n = lane & 15;
 
     const int blk = blockIdx.x;
-    int ti = 0;
-    if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
-    if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    int ti = 0, wtl = wave;  // wtl: the wave within its target's waves
+    if (GLU) {  // gate's waves, then up's, on the same tiles
+        ti = wave >= P.ks * P.tr ? 1 : 0;
+        wtl = wave - ti * P.ks * P.tr;
+    } else {
+        if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
+        if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    }
     // By value: a reference indexed by ti would reload its fields (dependent
     // scalar loads) at every use, including in the final reduction.
     const RqMmqTarget T = pick_target(P, ti);
     const int ks = P.ks;
-    const int tl = wave / ks, kpart = wave - (wave / ks) * ks;
+    const int tl = wtl / ks, kpart = wtl - (wtl / ks) * ks;
     const int tile = (blk - T.wg_start) * P.tr + tl;
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
@@ -570,7 +612,10 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     if (!DOTS) mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
     }  // column groups
     if (DOTS) return;
-    mmq_reduce<MP, G, NACC>(P, T);
+    if (GLU)
+        mmq_reduce_glu<MP, G, NACC>(P, T);
+    else
+        mmq_reduce<MP, G, NACC>(P, T);
 }
 
 // ---------------------------------------------------------------------------
@@ -611,7 +656,7 @@ __device__ __forceinline__ int q6_pair(u32 sc, int a, int b, int Da, int Db) {
     return __mul24(sbyte(sc, a), Da) + __mul24(sbyte(sc, b), Db);
 }
 
-template <int MP, int SBW, bool F32IN, bool DOTS, int G = 1>
+template <int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
 __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     constexpr int FMT = RQ_FMT_Q6_K;
     constexpr int NLD = 3 * SBW;               // code loads per lane
@@ -624,12 +669,17 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     const int g = lane >> 4, n = lane & 15;
 
     const int blk = blockIdx.x;
-    int ti = 0;
-    if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
-    if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    int ti = 0, wtl = wave;  // wtl: the wave within its target's waves
+    if (GLU) {  // gate's waves, then up's, on the same tiles
+        ti = wave >= P.ks * P.tr ? 1 : 0;
+        wtl = wave - ti * P.ks * P.tr;
+    } else {
+        if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
+        if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    }
     const RqMmqTarget T = pick_target(P, ti);
     const int ks = P.ks;
-    const int tl = wave / ks, kpart = wave - (wave / ks) * ks;
+    const int tl = wtl / ks, kpart = wtl - (wtl / ks) * ks;
     const int tile = (blk - T.wg_start) * P.tr + tl;
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
@@ -797,17 +847,20 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     }
     }  // column groups
     if (DOTS) return;
-    mmq_reduce<MP, G, NACC>(P, T);
+    if (GLU)
+        mmq_reduce_glu<MP, G, NACC>(P, T);
+    else
+        mmq_reduce<MP, G, NACC>(P, T);
 }
 
 // Kernel bodies by format. RQ_FMT_MIX_K: launches whose targets mix Q4_K
 // and Q6_K weights of one width (q, k and v of a Q4_K_M layer); a workgroup
 // serves one target, so it branches once, on that target's format, into its
 // body (staging included; the host sizes LDS for Q4_K's two planes).
-template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1>
+template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
 __device__ __forceinline__ void mmq_run(const RqMmqParams& P) {
     if constexpr (FMT == RQ_FMT_Q6_K) {
-        mmq6_body<MP, SBW, F32IN, DOTS, G>(P);
+        mmq6_body<MP, SBW, F32IN, DOTS, G, GLU>(P);
     } else if constexpr (FMT == RQ_FMT_MIX_K) {
         const int blk = blockIdx.x;
         int ti = 0;
@@ -819,7 +872,7 @@ __device__ __forceinline__ void mmq_run(const RqMmqParams& P) {
         else
             mmq_body<RQ_FMT_Q4_K, MP, SBW, F32IN, DOTS, G>(P);
     } else {
-        mmq_body<FMT, MP, SBW, F32IN, DOTS, G>(P);
+        mmq_body<FMT, MP, SBW, F32IN, DOTS, G, GLU>(P);
     }
 }
 
@@ -856,6 +909,33 @@ RQ_MMQ_SET(q4_k, RQ_FMT_Q4_K, 8)
 // Q6_K holds 48 B of codes per lane per super-block: sbw = 8 would need 96 registers of them.
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 2)
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 4)
+// Fused gate/up + activation + Q8_1 of the product (the reference's
+// mmq_glu_*), 4 super-blocks per wave (rows of up to 16: the two weights'
+// k-parts of two tiles fill at most 16 waves).
+#define RQ_MMQ_GLU_SET(NAME, FMT)                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_1(RqMmqParams p) {         \
+        mmq_run<FMT, 1, 4, false, false, 1, true>(p);                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_4(RqMmqParams p) {         \
+        mmq_run<FMT, 4, 4, false, false, 1, true>(p);                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_8(RqMmqParams p) {         \
+        mmq_run<FMT, 8, 4, false, false, 1, true>(p);                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_8x2(RqMmqParams p) {       \
+        mmq_run<FMT, 8, 4, false, false, 2, true>(p);                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_8x4(RqMmqParams p) {       \
+        mmq_run<FMT, 8, 4, false, false, 4, true>(p);                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqgluf_##NAME(RqMmqParams p) {            \
+        mmq_run<FMT, 1, 4, true, false, 1, true>(p);                                                 \
+    }
+RQ_MMQ_GLU_SET(q4_0, RQ_FMT_Q4_0)
+RQ_MMQ_GLU_SET(q8_0, RQ_FMT_Q8_0)
+RQ_MMQ_GLU_SET(q4_k, RQ_FMT_Q4_K)
+RQ_MMQ_GLU_SET(q6_k, RQ_FMT_Q6_K)
+
 // Mixed Q4_K / Q6_K launches (no block-dot variants: those run per weight).
 #define RQ_MMQ_MIX(MP, SBW)                                                                          \
     extern "C" __global__ __launch_bounds__(1024) void rq_mmq_q4_k_q6_k_##MP##_##SBW(RqMmqParams p) { \

@@ -190,6 +190,15 @@ struct RqMmqParams {
     int32_t kxp;
     int32_t pl_off;
     int32_t part_off;
+    int32_t h_off;       // rq_mmqglu_*: the product h of the workgroup's 32 rows (LDS)
+    // rq_mmqglu_* (gate and up as targets 0 and 1, each workgroup taking the
+    // same two 16-row tiles of both): h = act(x . gate) * (x . up) into hf
+    // (f32, column a at hf + a * n, may be null) and its Q8_1 (hq, hd, hs).
+    float* hf;
+    int8_t* hq;
+    uint16_t* hd;
+    uint16_t* hs;
+    int32_t act;
     int32_t pad;
 };
 

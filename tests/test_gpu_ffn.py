@@ -204,3 +204,28 @@ def test_gated_ffn_q8_1_input(gpuk, orc, tname, m):
         outs.append((gpuk.to_host(out, m * d), gpuk.to_host(gb, m * f)))
     assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32)), "h"
     assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32)), "out"
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q8_0", "Q4_0", "Q6_K"])
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 33])
+@pytest.mark.parametrize("act", ACTS)
+def test_gated_ffn_product_q8_1_is_exact(gpuk, orc, tname, m, act):
+    """The Q8_1 of the product that reaches the down projection (emitted by the
+    launch that computes h: dot4 rq_glu_*, MFMA rq_mmqglu_*, or rq_act_mul) is
+    bit-identical to rq_quantize_q8_1 of the f32 h written beside it: the
+    down projection's output equals rq_matvec on that quantization bit for
+    bit. Also h against the int8 oracle."""
+    t, d, f = TYPES[tname], 4096, 1024
+    gw = orc.random_weight(0xD0 + m, t, f, d)
+    uw = orc.random_weight(0xD1 + m, t, f, d)
+    dw = orc.random_weight(0xD2 + m, t, d, f)
+    g, u, dn = upload(gpuk, t, gw, f, d), upload(gpuk, t, uw, f, d), upload(gpuk, t, dw, d, f)
+    x = orc.normal(0xD3 + m, m * d, 0.0, 1.0)
+    out, gb, ub = gpuk.alloc(m * d), gpuk.alloc(m * f), gpuk.alloc(m * f)
+    gpuk.gated_ffn(gpuk.from_host(x), g, u, dn, act, out, gb, ub, m)
+    h = gpuk.to_host(gb, m * f)
+    qs, dq, _ = orc.quantize_q8_1(x, m, d)
+    orc.assert_close("h vs int8 oracle", orc.glu_q8_1(t, gw, uw, f, d, qs, dq, m, int(act)), h, 1e-3)
+    want = gpuk.alloc(m * d)
+    gpuk.matvec(gpuk.quantize_q8_1(gb, m, f), dn, want, m)
+    assert np.array_equal(gpuk.to_host(out, m * d).view(np.uint32), gpuk.to_host(want, m * d).view(np.uint32))
