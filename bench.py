@@ -251,8 +251,12 @@ def headline_kernel(name: str) -> bool:
     return name.startswith(KERNEL_PREFIX["mfma"]) or name == KERNEL_PREFIX["dot4"]
 
 
-def traffic_child() -> int:
-    """Run under rocprofv3 --pmc: a 64 MiB device copy (counter calibration), then 64 Q4_K matvec launches."""
+def traffic_child(argv) -> int:
+    """Run under rocprofv3 --pmc: a 64 MiB device copy (counter calibration),
+    then 64 matvec launches. `argv` after --traffic-child: nothing (the
+    headline: Q4_K 14336x4096, one column, default family) or `TYPE ROWS COLS
+    COLUMNS FAMILY` (e.g. 14 4096 14336 32 mfma), whose launches rotate over
+    enough weight copies to pass the 256 MB Infinity Cache."""
     import torch
 
     from oracle import oracle as orc
@@ -264,12 +268,17 @@ def traffic_child() -> int:
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    T, N, K = 12, 14336, 4096
-    w = gpu.upload(HostTensor("w", DType(T), (N, K), make_gguf(orc, T, N, K, 7)))
-    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(8, K)), 1, K)
-    out = gpu.alloc(N)
-    for _ in range(64):
-        gpu.matvec(xq, w, out, 1)
+    T, N, K, M, fam = 12, 14336, 4096, 1, None
+    if argv:
+        T, N, K, M, fam = int(argv[0]), int(argv[1]), int(argv[2]), int(argv[3]), argv[4]
+        gpu.set_kernels(fam)
+    wb = make_gguf(orc, T, N, K, 7)
+    copies = 1 if not argv else max(1, -(-(600 << 20) // wb.nbytes))
+    ws = [gpu.upload(HostTensor("w", DType(T), (N, K), wb)) for _ in range(copies)]
+    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(8, K * M)), M, K)
+    out = gpu.alloc(N * M)
+    for i in range(64):
+        gpu.matvec(xq, ws[i % copies], out, M)
     torch.cuda.synchronize()
     gpu.close()
     return 0
@@ -311,7 +320,7 @@ def measure_traffic() -> dict | None:
 
 def main() -> int:
     if "--traffic-child" in sys.argv:
-        return traffic_child()
+        return traffic_child(sys.argv[sys.argv.index("--traffic-child") + 1:])
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4096, help="timed matvec launches")
