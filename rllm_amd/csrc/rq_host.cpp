@@ -252,7 +252,9 @@ struct rq_ctx {
     size_t up_cap = 0;
     void* up_pin[2] = {};
     void* up_dev[2] = {};
-    hipEvent_t up_ev[2] = {};
+    hipEvent_t up_ev[2] = {};      // repack of staging buffer b done (the buffer is free)
+    hipEvent_t up_copied[2] = {};  // copy into staging buffer b done (pinned buffer b is free)
+    hipStream_t up_stream = nullptr;  // the uploads' host-to-device copies
     CopyPool* up_pool = nullptr;
 };
 
@@ -926,7 +928,9 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
             if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
             if (ctx->up_dev[b]) (void)hipFree(ctx->up_dev[b]);
             if (ctx->up_ev[b]) (void)hipEventDestroy(ctx->up_ev[b]);
+            if (ctx->up_copied[b]) (void)hipEventDestroy(ctx->up_copied[b]);
         }
+        if (ctx->up_stream) (void)hipStreamDestroy(ctx->up_stream);
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
         if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
         delete ctx;
@@ -1070,6 +1074,14 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         if (ctx->hq) (void)hipFree(ctx->hq);
         if (ctx->hd) (void)hipFree(ctx->hd);
         if (ctx->hs) (void)hipFree(ctx->hs);
+        if (ctx->up_stream) (void)hipStreamSynchronize(ctx->up_stream);
+        for (int b = 0; b < 2; b++) {
+            if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
+            if (ctx->up_dev[b]) (void)hipFree(ctx->up_dev[b]);
+            if (ctx->up_ev[b]) (void)hipEventDestroy(ctx->up_ev[b]);
+            if (ctx->up_copied[b]) (void)hipEventDestroy(ctx->up_copied[b]);
+        }
+        if (ctx->up_stream) (void)hipStreamDestroy(ctx->up_stream);
         if (ctx->mod) (void)hipModuleUnload(ctx->mod);
         if (ctx->mmq_mod) (void)hipModuleUnload(ctx->mmq_mod);
     }
@@ -1101,9 +1113,12 @@ static rq_status upload_staging(rq_ctx* ctx, size_t bytes) {
     }
     for (int b = 0; b < 2; b++) {
         if (!ctx->up_ev[b]) HIP_TRY(hipEventCreateWithFlags(&ctx->up_ev[b], hipEventDisableTiming));
+        if (!ctx->up_copied[b]) HIP_TRY(hipEventCreateWithFlags(&ctx->up_copied[b], hipEventDisableTiming));
     }
+    if (!ctx->up_stream) HIP_TRY(hipStreamCreateWithFlags(&ctx->up_stream, hipStreamNonBlocking));
     if (ctx->up_cap >= bytes) return RQ_OK;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->up_stream));
     for (int b = 0; b < 2; b++) {
         if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
         if (ctx->up_dev[b]) (void)hipFree(ctx->up_dev[b]);
@@ -1195,19 +1210,25 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
         delete w;
         return st;
     }
-    // Two chunks in flight: while the DMA engine copies chunk i out of one
-    // pinned buffer (and the repack kernel follows it on the stream), the
-    // host threads fill the other with chunk i + 1.
+    // Two chunks in flight, three engines busy: the host threads fill one
+    // pinned buffer with chunk i + 1 while the DMA engine copies chunk i (on
+    // the upload stream) and the repack of chunk i - 1 runs on the context's
+    // stream. Events hand the buffers over: a pinned buffer is refilled once
+    // its copy is done, a staging buffer is copied into once its repack is.
     for (int64_t row0 = 0, i = 0; row0 < rows && st == RQ_OK; row0 += chunk_rows, i++) {
         const int b = (int)(i & 1);
         const int64_t n = std::min(chunk_rows, rows - row0);
-        if (i >= 2 && (e = hipEventSynchronize(ctx->up_ev[b])) != hipSuccess) {
+        if (i >= 2 && (e = hipEventSynchronize(ctx->up_copied[b])) != hipSuccess) {
             st = hip_fail("hipEventSynchronize", e);
             break;
         }
         ctx->up_pool->copy(ctx->up_pin[b], (const uint8_t*)gguf + row0 * rb, (size_t)(n * rb));
-        e = hipMemcpyAsync(ctx->up_dev[b], ctx->up_pin[b], (size_t)(n * rb), hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = hipEventRecord(ctx->up_ev[b], ctx->stream);
+        e = i >= 2 ? hipStreamWaitEvent(ctx->up_stream, ctx->up_ev[b], 0) : hipSuccess;
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(ctx->up_dev[b], ctx->up_pin[b], (size_t)(n * rb), hipMemcpyHostToDevice,
+                               ctx->up_stream);
+        if (e == hipSuccess) e = hipEventRecord(ctx->up_copied[b], ctx->up_stream);
+        if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, ctx->up_copied[b], 0);
         if (e != hipSuccess) {
             st = hip_fail("hipMemcpyAsync", e);
             break;
@@ -1240,9 +1261,14 @@ extern "C" rq_status rq_upload(rq_ctx* ctx, int type, int64_t rows, int64_t cols
             p.k = (int32_t)cols;
             st = launch(ctx, ctx->repack[fmt], "rq_repack", (uint64_t)((n * p.S + RQ_THREADS - 1) / RQ_THREADS), &p);
         }
+        if (st == RQ_OK && (e = hipEventRecord(ctx->up_ev[b], ctx->stream)) != hipSuccess)
+            st = hip_fail("hipEventRecord", e);
     }
-    // The staging buffers are reused by the next upload: wait for this one.
+    // The staging buffers are reused by the next upload: wait for this one
+    // (the context's stream waited for every copy).
     e = hipStreamSynchronize(ctx->stream);
+    const hipError_t e2 = hipStreamSynchronize(ctx->up_stream);
+    if (e == hipSuccess) e = e2;
     if (st == RQ_OK && e != hipSuccess) st = hip_fail("hipStreamSynchronize", e);
     if (st != RQ_OK) {
         (void)hipFree(w->base);
