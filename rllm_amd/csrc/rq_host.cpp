@@ -588,10 +588,9 @@ hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int g, int sbw, boo
 }
 
 void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
-    const int NB = 8 * S2;
     L.kxp = S2 * 256 + 64;  // 64 B of skew: columns start on different LDS banks
     L.pl_off = L.mp * L.kxp;
-    L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * NB * 4;
+    L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * RQ_MMQ_NBP(S2) * 4;
     L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4);
 }
 

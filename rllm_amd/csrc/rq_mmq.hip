@@ -76,7 +76,8 @@ __device__ __forceinline__ float half_f(u32 w, int i) { return h2f(i ? (w >> 16)
 // ---------------------------------------------------------------------------
 // Activation staging. Per (column a, 32-element block b): the codes at
 // a * kxp + 32 b, and per-block planes of floats, plane p at
-// pl_off + ((p * MP + a) * NB + b) * 4 (NB = 8 * S2 blocks per padded row):
+// pl_off + ((p * MP + a) * NBP + b) * 4 (8 * S2 blocks per padded row, column
+// stride NBP = RQ_MMQ_NBP(S2)):
 //   Q4_K  dxe = dx (dx / 16 in high windows), f8 = 8 dx sum q
 //   Q4_0  dxe as Q4_K, fo = -8 dx sum q in low windows (else 0)
 //   Q8_0, Q6_K  dx
@@ -88,9 +89,9 @@ __device__ __forceinline__ float half_f(u32 w, int i) { return h2f(i ? (w >> 16)
 template <int FMT, int MP, bool DOTS>
 __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b, int sq, float dx) {
     constexpr int NPL = MF<FMT>::NPL;
-    const int NB = 8 * P.S2;
-    const int stride = MP * NB * 4;
-    char* pl = mmq_lds + P.pl_off + (a * NB + b) * 4;
+    const int NBP = RQ_MMQ_NBP(P.S2);
+    const int stride = MP * NBP * 4;
+    char* pl = mmq_lds + P.pl_off + (a * NBP + b) * 4;
     const bool hi = (b >> 1) & 1;
     if (FMT == RQ_FMT_Q4_K) {
         *(float*)pl = hi ? dx * 0.0625f : dx;
@@ -463,13 +464,14 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
         for (int wp = 0; wp < NPH; wp++) A[wp] = v4i{0, 0, 0, 0};
 
-        const int stride = MP * NB * 4;  // bytes between planes
+        const int NBP = RQ_MMQ_NBP(S2);
+        const int stride = MP * NBP * 4;  // bytes between planes
         // The lane's plane addresses at this k-part's first block (each
         // D-group then reads at compile-time offsets from them): mp <= 4 one
         // activation, mp = 8 two (2 g, 2 g + 1).
         const int a_lane = MP == 1 ? 0 : MP == 2 ? (g >> 1) : MP == 4 ? g : 2 * g;
         const int lb_lane = MP == 1 ? 4 * g : MP == 2 ? 4 * (g & 1) : 0;
-        const char* plb = mmq_lds + P.pl_off + (a_lane * NB + sb0 * 8 + lb_lane) * 4;
+        const char* plb = mmq_lds + P.pl_off + (a_lane * NBP + sb0 * 8 + lb_lane) * 4;
         float sbd[2] = {0.f, 0.f}, sbm[2] = {0.f, 0.f};  // Q4_K: the current super-block's sums
 #pragma unroll
         for (int t = 0; t < ND; t++) {
@@ -521,7 +523,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                     const int a = MP == 8 ? 2 * g + (v >> 1) : (MP == 1 ? 0 : MP == 2 ? (g >> 1) : g);
                     const int b = pb + (MP == 8 ? (v & 1) : v);
                     const bool hi = (b >> 1) & 1;
-                    const int sq = *(const int*)(mmq_lds + P.pl_off + MF<FMT>::NPL * stride + (a * NB + b) * 4);
+                    const int sq = *(const int*)(mmq_lds + P.pl_off + MF<FMT>::NPL * stride + (a * NBP + b) * 4);
                     int dot = D[v];
                     if (FMT == RQ_FMT_Q4_K) dot = hi ? (dot >> 4) + 8 * sq : dot;
                     if (FMT == RQ_FMT_Q4_0) dot = hi ? (dot >> 4) : dot - 8 * sq;
@@ -572,7 +574,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
                 const bool hiw = t & 1;
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    const char* pe = plb + e * NB * 4 + 8 * t;
+                    const char* pe = plb + e * NBP * 4 + 8 * t;
                     const float2 p0 = *(const float2*)pe;
                     const float pv0[2] = {p0.x, p0.y};
                     if (FMT == RQ_FMT_Q4_K) {
@@ -753,7 +755,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
         // activation 0, blocks 2g, 2g + 1 of each super-block; mp = 4
         // activation g; mp = 8 activations 2g, 2g + 1.
         const int a_lane = MP == 1 ? 0 : (MP == 4 ? g : 2 * g);
-        const char* plb = mmq_lds + P.pl_off + (a_lane * NB + sb0 * 8 + (MP == 1 ? 2 * g : 0)) * 4;
+        const char* plb = mmq_lds + P.pl_off + (a_lane * RQ_MMQ_NBP(S2) + sb0 * 8 + (MP == 1 ? 2 * g : 0)) * 4;
         const int row = tile * 16 + n, U16 = P.k >> 4;
         int32_t* dots = (int32_t*)T.out;
 
@@ -829,7 +831,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
                         }
 #pragma unroll
                         for (int e = 0; e < 2; e++) {
-                            const float2 p = *(const float2*)(plb + e * NB * 4 + 4 * (8 * i + 2 * w));
+                            const float2 p = *(const float2*)(plb + e * RQ_MMQ_NBP(S2) * 4 + 4 * (8 * i + 2 * w));
                             acc[e] = fmaf(p.x, (float)q6_pair(sc, 0, 1, D0[2 * e], D0[2 * e + 1]), acc[e]);
                             acc[e] = fmaf(p.y, (float)q6_pair(sc, 2, 3, D1[2 * e], D1[2 * e + 1]), acc[e]);
                         }

@@ -163,6 +163,12 @@ struct RqDotsParams {
 // Super-blocks per wave of an rq_mmq launch (RqMmqParams.ks waves per tile).
 #define RQ_MMQ_SBW_MAX 4
 
+// Floats per activation column in one staged per-block plane of an rq_mmq
+// workgroup: the column's 8 * S2 blocks and 4 of skew, so the columns of a
+// plane start 16 bytes apart in the LDS banks (a column stride of 8 * S2
+// floats alone is a multiple of the bank width) and float4 reads stay aligned.
+#define RQ_MMQ_NBP(S2) (8 * (S2) + 4)
+
 struct RqMmqTarget {
     const uint8_t* code;  // code plane
     const uint8_t* hdr;   // header plane
