@@ -244,6 +244,24 @@ __device__ __forceinline__ Scales<FMT, MP> scales_of(const int4 h, bool hsel, in
     return r;
 }
 
+// One Q4_K super-block header (row n's 16 bytes) decoded for the MFMA
+// bodies: k[0], k[1] = the scales and mins of blocks 0-3 as bytes, k[2], k[3]
+// those of blocks 4-7 (scales_of's words); f = d, dmin. The words pass through
+// an empty asm so that they stay whole in registers and each block's value is
+// one byte conversion (folded into the uses, the masks become a bit-field
+// extract per value and are repeated per column group).
+__device__ __forceinline__ void q4k_decode(const int4 h, u32 (&k)[4], float (&f)[2]) {
+    const u32 b0 = (u32)h.y, b1 = (u32)h.z, b2 = (u32)h.w;
+    f[0] = h2f((u32)h.x & 0xFFFFu);
+    f[1] = h2f((u32)h.x >> 16);
+    k[0] = b0 & 0x3F3F3F3Fu;
+    k[1] = b1 & 0x3F3F3F3Fu;
+    k[2] = (b2 & 0x0F0F0F0Fu) | ((b0 >> 2) & 0x30303030u);
+    k[3] = ((b2 >> 4) & 0x0F0F0F0Fu) | ((b1 >> 2) & 0x30303030u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) asm volatile("" : "+v"(k[i]));
+}
+
 // Target ti of a launch, by value (see sgpr_value).
 __device__ __forceinline__ RqMmqTarget pick_target(const RqMmqParams& P, int ti) {
     RqMmqTarget r;
@@ -386,7 +404,6 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr int NH = MP == 1 ? SBW / 2 : SBW;  // header loads per lane
     constexpr int NACC = MP == 8 ? 2 : 1;
 
-    const int threads = blockDim.x;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -409,7 +426,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     const int tile = (blk - T.wg_start) * P.tr + tl;
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
-    const int S2 = P.S2, NB = 8 * S2;
+    const int S2 = P.S2;
     const int sb0 = kpart * SBW;           // first super-block of the part
     const int nsb = min(SBW, S2 - sb0);    // even, >= 2
 
@@ -442,6 +459,11 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    // Q4_K: the lane's decoded headers (q4k_decode), filled by column group 0
+    // at each super-block's first D-group and reused by the later groups.
+    u32 kq[NH][4];
+    float kf[NH][2];
 
     // ---- Staging writes (the LDS writes wait only for the staging loads).
 #pragma unroll
@@ -512,7 +534,19 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
             const int jb = MP == 8 ? 2 * (t & 3) : 0;
             const int lb0 = MP == 1 ? 16 * t + 4 * g : MP == 2 ? 8 * t + 4 * (g & 1) : MP == 4 ? 4 * t : 2 * t;
             const int hidx = MP == 1 ? t : (t * NPH) / 4;  // header (super-block) of this D-group
-            const Scales<FMT, MP> sc = scales_of<FMT, MP>(hv[hidx], hsel != 0, jb);
+            Scales<FMT, MP> sc;
+            if (FMT == RQ_FMT_Q4_K) {
+                const bool first = t == 0 || hidx != (MP == 1 ? t - 1 : ((t - 1) * NPH) / 4);
+                if (gi == 0 && first) q4k_decode(hv[hidx], kq[hidx], kf[hidx]);
+                const bool second = MP == 8 ? jb >= 4 : hsel != 0;
+                sc.d = kf[hidx][0];
+                sc.dmin = kf[hidx][1];
+                sc.sc = second ? kq[hidx][2] : kq[hidx][0];
+                sc.mn = second ? kq[hidx][3] : kq[hidx][1];
+                sc.dw0 = sc.dw1 = 0;
+            } else {
+                sc = scales_of<FMT, MP>(hv[hidx], hsel != 0, jb);
+            }
             const int pb = sb0 * 8 + lb0;  // first block (global index within the padded row)
 
             if (DOTS) {
@@ -685,7 +719,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     const int tile = (blk - T.wg_start) * P.tr + tl;
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
-    const int S2 = P.S2, NB = 8 * S2;
+    const int S2 = P.S2;
     const int sb0 = kpart * SBW;
     const int nsb = min(SBW, S2 - sb0);
 
