@@ -531,13 +531,16 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
     const int U = (k + 31) >> 5;
     const int total = NC * 8 * S;
     if (F32IN) {
+        // The second round only when the workgroup has items for it (a wide
+        // workgroup stages a 4096-wide column in one round); uniform.
+        const bool two = total > QITEMS;
         QItem q0, q1;
         qitem_load(xf, k, total, S, U, 0, q0);
-        qitem_load(xf, k, total, S, U, QITEMS, q1);
+        if (two) qitem_load(xf, k, total, S, U, QITEMS, q1);
         load_w();
         __builtin_amdgcn_sched_barrier(0);
         qitem_write<FMT>(q0, S);
-        qitem_write<FMT>(q1, S);
+        if (two) qitem_write<FMT>(q1, S);
         for (int base = 2 * QITEMS; base < total; base += QITEMS) {  // uniform trip count
             QItem q;
             qitem_load(xf, k, total, S, U, base, q);
