@@ -103,9 +103,13 @@ class HipWeight:
         return {_lib.KERNELS_MFMA: "mfma", _lib.KERNELS_BOTH: "both"}.get(f.value, "dot4")
 
     def free(self) -> None:
+        """rq_weight_free. After the backend was closed (rq_close freed the
+        device memory and detached the handle) this only deletes the handle."""
         if self.handle:
             h, self.handle = self.handle, None
-            _lib.check(_lib.lib().rq_weight_free(h))
+            st = _lib.lib().rq_weight_free(h)
+            if getattr(self._backend, "ctx", None) is not None:
+                _lib.check(st)
 
     def __del__(self):
         try:
@@ -202,14 +206,16 @@ class HipBackend:
         return HipWeight(self, h.value, dtype, rows, cols, t.name)
 
     def upload_gguf(self, g, name: str) -> HipWeight:
-        """load_weight + Backend::upload of a named 2-D quantized tensor straight
-        from a mapped GGUF file (`rllm_amd.gguf.GgufFile`; rq_gguf_upload)."""
+        """load_weight + Backend::upload of a named quantized tensor straight
+        from a mapped GGUF file (`rllm_amd.gguf.GgufFile`; rq_gguf_upload),
+        seen as 2-D as HostTensor::as_2d does (outer dims fold into rows)."""
         info = g.require_tensor(name)
         dtype = DType.from_ggml(info.type)
         h = ctypes.c_void_p()
         _lib.check(_lib.lib().rq_gguf_upload(self.ctx, g.handle, name.encode(), ctypes.byref(h)))
-        rows, cols = (info.dims[1], info.dims[0]) if len(info.dims) == 2 else (0, 0)
-        return HipWeight(self, h.value, dtype, rows, cols, name)
+        rows, cols = ctypes.c_int64(), ctypes.c_int64()
+        _lib.check(_lib.lib().rq_weight_shape(h.value, None, ctypes.byref(rows), ctypes.byref(cols), None))
+        return HipWeight(self, h.value, dtype, rows.value, cols.value, name)
 
     def weight_to_gguf(self, w: HipWeight) -> np.ndarray:
         out = np.empty(w.rows * w.dtype.row_bytes(w.cols), dtype=np.uint8)

@@ -135,3 +135,60 @@ def test_layer_graph_replays(gpu, orc):
         want = [gpu.to_host(o).copy() for o in e_outs] + [gpu.to_host(e_ffn).copy(), gpu.to_host(x).copy()]
         for i, (a, b) in enumerate(zip(got, want)):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep} output {i}"
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_upload_during_capture_is_refused(orc):
+    """rq_upload allocates and synchronizes: while the context's stream
+    captures it fails before any stream work (nothing is recorded), and
+    uploads work again after the capture."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    from rllm_amd.errors import RllmError
+
+    fresh = HipBackend(0)
+    try:
+        k, n = 512, 32
+        w = make_weight(orc, 12, n, k, 6, "normal")
+        with pytest.raises(RllmError, match="capturing"):
+            _capture(fresh, lambda: upload(fresh, 12, w, n, k))
+        torch.cuda.synchronize()
+        wg = upload(fresh, 12, w, n, k)
+        assert np.array_equal(fresh.weight_to_gguf(wg), w)
+        del wg
+    finally:
+        fresh.synchronize()
+        fresh.close()
+
+
+def test_weight_outlives_context(gpu, orc):
+    """rq_close frees the device memory of weights still live and detaches
+    them: a later call with such a weight fails cleanly (no read of freed
+    memory), rq_weight_free only deletes the handle and reports it, and a
+    weight of another live context is refused too."""
+    from rllm_amd import _lib
+    from rllm_amd.errors import RllmError
+
+    k, n = 512, 32
+    w = make_weight(orc, 12, n, k, 8, "normal")
+    fresh = HipBackend(0)
+    wf = upload(fresh, 12, w, n, k)
+    kept = upload(fresh, 12, w, n, k)
+    kept.free()  # freed before the close: the ordinary path
+    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(9, k)), 1, k)
+    out = gpu.alloc(n)
+    with pytest.raises(RllmError, match="another context"):
+        gpu.matvec(xq, wf, out, 1)
+    fresh.synchronize()
+    fresh.close()
+    with pytest.raises(RllmError, match="context was closed"):
+        gpu.matvec(xq, wf, out, 1)
+    h, wf.handle = wf.handle, None
+    assert _lib.lib().rq_weight_free(h) == _lib.RQ_ERR_INVALID
+    assert "context was closed" in _lib.last_error()
+    # The Python handle of a closed backend frees quietly.
+    fresh2 = HipBackend(0)
+    w2 = upload(fresh2, 12, w, n, k)
+    fresh2.close()
+    w2.free()
+    assert w2.handle is None
