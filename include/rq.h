@@ -189,6 +189,23 @@ rq_status rq_matmul(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const
 rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* const* ws,
                          float* const* outs, const int64_t* out_lens, int count);
 
+/* Most activation values (m * k) rq_matmul_many_noalloc takes: the capacity
+ * of its fixed device scratch (2 MiB of codes + 2 x 64 KiB of f16 scales). */
+#define RQ_NOALLOC_MAX_VALUES (1 << 21)
+
+/* rq_matmul_many without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, launches and results (bit for bit) as rq_matmul_many; for
+ * m >= 2 the Q8_1 copy of x goes to a fixed device array of the library
+ * (one per device, RQ_NOALLOC_MAX_VALUES values, held until the process
+ * ends) instead of the context's scratch, so nothing is allocated even
+ * before rq_reserve. m * k > RQ_NOALLOC_MAX_VALUES fails with RQ_ERR_SHAPE.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (other streams, other contexts, other threads) race. */
+rq_status rq_matmul_many_noalloc(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* const* ws,
+                                 float* const* outs, const int64_t* out_lens, int count);
+
 /* Sizes the context's Q8_1 scratches, for rq_matmul* activations (m * k,
  * m >= 2) and rq_gated_ffn products (m * n_ffn), to `values` elements each,
  * so later calls allocate nothing (graph capture;

@@ -21,6 +21,7 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "rq.h")
 
 RQ_OK, RQ_ERR_SHAPE, RQ_ERR_BACKEND, RQ_ERR_UNSUPPORTED, RQ_ERR_INVALID, RQ_ERR_GGUF = 0, 1, 2, 3, 4, 5
 MATVEC_MAX_COLS = 8
+NOALLOC_MAX_VALUES = 1 << 21  # RQ_NOALLOC_MAX_VALUES
 # Kernel families (rq_set_kernels).
 KERNELS_AUTO, KERNELS_DOT4, KERNELS_MFMA, KERNELS_BOTH = 0, 1, 2, 3
 KERNEL_FAMILIES = {"auto": KERNELS_AUTO, "dot4": KERNELS_DOT4, "mfma": KERNELS_MFMA, "both": KERNELS_BOTH}
@@ -85,6 +86,8 @@ _SIGNATURES = {
     "rq_matmul": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _i64]),
     "rq_matmul_many": (_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                               ctypes.POINTER(_i64), _int]),
+    "rq_matmul_many_noalloc": (_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                      ctypes.POINTER(_i64), _int]),
     "rq_reserve": (_int, [_vp, _i64]),
     "rq_block_dots": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
     "rq_set_kernels": (_int, [_vp, _int]),

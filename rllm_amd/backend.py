@@ -267,6 +267,17 @@ class HipBackend:
                                              _ptrs([o.data_ptr() for o in outs]), _i64s([o.numel() for o in outs]),
                                              len(ws)))
 
+    def matmul_many_noalloc(self, x: torch.Tensor, ws: Sequence[HipWeight], outs: Sequence[torch.Tensor],
+                            m: int) -> None:
+        """matmul_many that allocates nothing: the m >= 2 Q8_1 copy of x goes to
+        the library's fixed device array (m * k <= NOALLOC_MAX_VALUES), not the
+        context's scratch (rq_matmul_many_noalloc; no reference counterpart)."""
+        if len(ws) != len(outs) or not ws:
+            raise ShapeError(f"matmul_many: {len(ws)} weights, {len(outs)} outputs")
+        _lib.check(_lib.lib().rq_matmul_many_noalloc(self.ctx, x.data_ptr(), x.numel(), m,
+                                                     _ptrs([w.handle for w in ws]), _ptrs([o.data_ptr() for o in outs]),
+                                                     _i64s([o.numel() for o in outs]), len(ws)))
+
     # ---- gated FFN -------------------------------------------------------------
 
     def act_mul(self, act: Activation, gate: torch.Tensor, up: torch.Tensor, length: int, hq: Q8_1 | None = None) -> None:

@@ -4,7 +4,10 @@
    pass and the dot4 matvecs; csrc/rq_mmq.hip: the int8-MFMA matvecs) into
    one gfx950 code object.
 2. An assembler stub (.incbin) embeds the code objects in the library.
-3. g++ compiles the host side (csrc/rq_host.cpp) against the HIP runtime.
+3. hipcc compiles csrc/rq_static.hip (the fixed device scratch of
+   rq_matmul_many_noalloc) as an ordinary host + device object.
+4. g++ compiles the host side (csrc/rq_host.cpp) against the HIP runtime and
+   links everything into the library.
 
 The result, rllm_amd/lib/librq.so, is self-contained: rq_open() loads the
 embedded code objects with hipModuleLoadData; nothing is compiled at run time.
@@ -70,11 +73,16 @@ def build(verbose: bool = False) -> str:
     stub.append('    .section .note.GNU-stack,"",@progbits\n')
     with open(blob, "w") as f:
         f.write("".join(stub))
+    # The fixed scratch of rq_matmul_many_noalloc: a device array in a HIP
+    # translation unit of its own (host + gfx950 device code, registered with
+    # the HIP runtime when the library loads).
+    static_obj = os.path.join(BUILD, "rq_static.o")
+    _run([hipcc, "-c", "-fPIC", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_static.hip"), "-o", static_obj])
     tmp = LIB + ".tmp"
     _run([
         "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{CSRC}",
-        os.path.join(CSRC, "rq_host.cpp"), os.path.join(CSRC, "rq_gguf.cpp"), blob,
+        os.path.join(CSRC, "rq_host.cpp"), os.path.join(CSRC, "rq_gguf.cpp"), blob, static_obj,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
         "-o", tmp,
     ])

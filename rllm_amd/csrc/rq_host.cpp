@@ -29,6 +29,9 @@
 
 extern "C" const unsigned char rq_kernels_blob[];  // rq_kernels.hip: Q8_1 pass, dot4 matvecs
 extern "C" const unsigned char rq_mmq_blob[];      // rq_mmq.hip: int8-MFMA matvecs
+// rq_static.hip: the device address of the fixed scratch of
+// rq_matmul_many_noalloc on the current device.
+extern "C" __attribute__((visibility("hidden"))) hipError_t rq_noalloc_scratch(int device, void** ptr, size_t* bytes);
 
 namespace {
 
@@ -261,6 +264,12 @@ struct rq_ctx {
     // memory and detaches them (their handles then only accept
     // rq_weight_free, rq_weight_shape and rq_weight_kernels).
     std::unordered_set<rq_weight*> live;
+    // The fixed Q8_1 scratch of rq_matmul_many_noalloc on this device (the
+    // library's static device array, resolved at rq_open), or the HIP error
+    // that resolving it gave.
+    uint8_t* na_base = nullptr;
+    size_t na_bytes = 0;
+    hipError_t na_err = hipSuccess;
 };
 
 struct rq_weight {
@@ -953,6 +962,13 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     hipDeviceProp_t prop;
     if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return bail(hip_fail("hipGetDeviceProperties", e));
     ctx->cus = prop.multiProcessorCount;
+    // The no-allocation entry point's scratch, resolved once per device with
+    // the device current; a failure only disables that entry point.
+    {
+        void* na = nullptr;
+        ctx->na_err = rq_noalloc_scratch(device, &na, &ctx->na_bytes);
+        ctx->na_base = (uint8_t*)na;
+    }
     ctx->lds_wide = (int)std::min<size_t>(prop.sharedMemPerBlock, size_t(160) << 10);
     snprintf(ctx->arch, sizeof ctx->arch, "%.63s", prop.gcnArchName);
     if (strncmp(ctx->arch, "gfx950", 6) != 0)
@@ -1570,6 +1586,24 @@ rq_status matmul_many_run(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m,
 extern "C" rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* const* ws,
                                     float* const* outs, const int64_t* out_lens, int count) {
     return matmul_many_run(ctx, x, x_len, m, ws, outs, out_lens, count, nullptr);
+}
+
+extern "C" rq_status rq_matmul_many_noalloc(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m,
+                                            const rq_weight* const* ws, float* const* outs, const int64_t* out_lens,
+                                            int count) {
+    if (!ctx || !ws || count < 1 || !ws[0]) return matmul_many_run(ctx, x, x_len, m, ws, outs, out_lens, count, nullptr);
+    if (ctx->na_err != hipSuccess)
+        return hip_fail("matmul_many_noalloc: hipGetSymbolAddress(scratch)", ctx->na_err);
+    const int64_t values = m * ws[0]->cols;
+    if (m > 0 && values > (int64_t)RQ_NOALLOC_MAX_VALUES)
+        return fail(RQ_ERR_SHAPE, "matmul_many_noalloc: %lld activation values (m = %lld, k = %lld) exceed the fixed "
+                    "scratch of %d", (long long)values, (long long)m, (long long)ws[0]->cols, RQ_NOALLOC_MAX_VALUES);
+    // Planes of the fixed array (rq_static.hip): codes, then f16 d, then f16 s.
+    const size_t dplane = (size_t)RQ_NOALLOC_MAX_VALUES, splane = dplane + (size_t)RQ_NOALLOC_MAX_VALUES / 32 * 2;
+    if (!ctx->na_base || ctx->na_bytes < splane + (size_t)RQ_NOALLOC_MAX_VALUES / 32 * 2)
+        return fail(RQ_ERR_BACKEND, "matmul_many_noalloc: fixed scratch unavailable");
+    const Q8Scratch fixed{(int8_t*)ctx->na_base, (uint16_t*)(ctx->na_base + dplane), (uint16_t*)(ctx->na_base + splane)};
+    return matmul_many_run(ctx, x, x_len, m, ws, outs, out_lens, count, &fixed);
 }
 
 extern "C" rq_status rq_matmul(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, const rq_weight* w, float* out,
