@@ -25,6 +25,9 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "librq.so")
+# bench.py's roofline reference (a read-only kernel of the matvec's launch
+# shape); not part of librq.so.
+FLOOR_LIB = os.path.join(LIBDIR, "librq_floor.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 # Kernel sources, one code object each (embedded as <name>_blob).
@@ -87,8 +90,12 @@ def build(verbose: bool = False) -> str:
         "-o", tmp,
     ])
     os.replace(tmp, LIB)
+    # bench.py's read-floor probe (rq_floor.hip), a library of its own.
+    floor_tmp = FLOOR_LIB + ".tmp"
+    _run([hipcc, "-shared", "-fPIC", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_floor.hip"), "-o", floor_tmp])
+    os.replace(floor_tmp, FLOOR_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {FLOOR_LIB}")
     return LIB
 
 

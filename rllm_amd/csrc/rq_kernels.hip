@@ -498,6 +498,24 @@ __device__ __forceinline__ void qitem_write(QItem& q, int S) {
     }
 }
 
+// An empty asm over the 16-byte chunks sub-block j of a super-block reads:
+// the chunks count as used (waited for) here, and code that reads them cannot
+// move above this point.
+__device__ __forceinline__ void pin4(int4& v) { __asm__ volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+
+template <int FMT>
+__device__ __forceinline__ void pin_sub(SB<FMT>& w, int j) {
+    if (FMT == RQ_FMT_Q8_0) {
+        pin4(w.c[1 + 2 * j]);
+        pin4(w.c[2 + 2 * j]);
+    } else if (FMT == RQ_FMT_Q6_K) {
+        pin4(w.c[1 + j]);
+        if ((j & 1) == 0) pin4(w.c[9 + (j >> 1)]);
+    } else {
+        pin4(w.c[1 + j]);
+    }
+}
+
 // Dot of one super-block slot with nc columns, accumulated into acc.
 template <int FMT, int NC>
 __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool active, float* acc) {
@@ -506,13 +524,37 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
     for (int c = 0; c < NC; c++) {
         const char* rec = lds_rec(rq_lds, S, c, s);
         float accd = 0.f, accm = 0.f;
+        if (NC == 1) {
+            // One column: sub-block j's dot and its scaling run as soon as
+            // its chunks have arrived (the weight chunks retire in order), so
+            // the work left after the last chunk is one sub-block's; the
+            // activation block j + 1 is read from LDS meanwhile. Left to
+            // itself the compiler defers all eight scalings past the last
+            // load; the empty asm statements (ordered among themselves) fix
+            // where each chunk is first used and where each step of the
+            // accumulation has to be done.
+            SB<FMT> wp = w;
+            XJ xn;
+            lds_read_x(rec, 0, xn);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            XJ x;
-            lds_read_x(rec, j, x);
-            int s0, s1;
-            sub_dot<FMT>(w, j, x, s0, s1);
-            sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
+            for (int j = 0; j < 8; j++) {
+                const XJ x = xn;
+                if (j < 7) lds_read_x(rec, j + 1, xn);
+                pin_sub<FMT>(wp, j);
+                int s0, s1;
+                sub_dot<FMT>(wp, j, x, s0, s1);
+                sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
+                __asm__ volatile("" : "+v"(accd), "+v"(accm));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                XJ x;
+                lds_read_x(rec, j, x);
+                int s0, s1;
+                sub_dot<FMT>(w, j, x, s0, s1);
+                sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
+            }
         }
         const float v = sb_finish<FMT>(sc, accd, accm);
         acc[c] += active ? v : 0.f;
@@ -547,6 +589,9 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
             qitem_write<FMT>(q, S);
         }
     } else {
+        // Every thread loads two items (clamped to the last one past the end:
+        // cache hits), unconditionally: loads under a branch made the
+        // compiler wait for them at the join, before the weight loads.
         StageItem si0 = stage_item<NC>(threadIdx.x, total, S, U);
         StageItem si1 = stage_item<NC>(threadIdx.x + THREADS, total, S, U);
         XJ x0, x1;
