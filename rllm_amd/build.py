@@ -46,23 +46,51 @@ HIPCC_FLAGS = [
 ]
 
 
+def _check(cmd: list[str], returncode: int, output: str) -> None:
+    out = "\n".join(l for l in output.splitlines() if "packed-fp32-ops" not in l)
+    if returncode != 0:
+        raise RuntimeError(f"build step failed ({returncode}): {' '.join(cmd)}\n{out}")
+
+
 def _run(cmd: list[str]) -> None:
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
-    if r.returncode != 0:
-        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    _check(cmd, r.returncode, r.stdout)
 
 
-def build(verbose: bool = False) -> str:
-    """Compile everything; returns the library path."""
-    os.makedirs(BUILD, exist_ok=True)
-    os.makedirs(LIBDIR, exist_ok=True)
+def _run_all(cmds: list[list[str]]) -> None:
+    """Runs independent compile steps at once; fails on the first failure."""
+    procs = [(c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)) for c in cmds]
+    results = [(c, p.communicate()[0], p.returncode) for c, p in procs]
+    for c, out, rc in results:
+        _check(c, rc, out)
+
+
+def build(verbose: bool = False, csrc: str = CSRC, libdir: str = LIBDIR, builddir: str = BUILD,
+          floor: bool = True) -> str:
+    """Compile everything; returns the library path. `csrc`, `libdir` and
+    `builddir` default to the package's own (a build of another source tree
+    goes elsewhere); the kernel sources compile in parallel."""
+    os.makedirs(builddir, exist_ok=True)
+    os.makedirs(libdir, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    blob = os.path.join(BUILD, "rq_blob.S")
+    lib = os.path.join(libdir, "librq.so")
+    blob = os.path.join(builddir, "rq_blob.S")
+    static_obj = os.path.join(builddir, "rq_static.o")
+    jobs = [[hipcc, "--genco", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, f"{name}.hip"), "-o",
+             os.path.join(builddir, f"{name}.hsaco")] for name in KERNEL_SOURCES]
+    # The fixed scratch of rq_matmul_many_noalloc: a device array in a HIP
+    # translation unit of its own (host + gfx950 device code, registered with
+    # the HIP runtime when the library loads).
+    jobs.append([hipcc, "-c", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_static.hip"), "-o", static_obj])
+    floor_lib = os.path.join(libdir, "librq_floor.so")
+    if floor:
+        # bench.py's read-floor probe (rq_floor.hip), a library of its own.
+        jobs.append([hipcc, "-shared", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_floor.hip"), "-o",
+                     floor_lib + ".tmp"])
+    _run_all(jobs)
     stub = []
     for name in KERNEL_SOURCES:
-        hsaco = os.path.join(BUILD, f"{name}.hsaco")
-        _run([hipcc, "--genco", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, f"{name}.hip"), "-o", hsaco])
+        hsaco = os.path.join(builddir, f"{name}.hsaco")
         stub += [
             "    .section .rodata\n",
             "    .balign 4096\n",
@@ -76,27 +104,20 @@ def build(verbose: bool = False) -> str:
     stub.append('    .section .note.GNU-stack,"",@progbits\n')
     with open(blob, "w") as f:
         f.write("".join(stub))
-    # The fixed scratch of rq_matmul_many_noalloc: a device array in a HIP
-    # translation unit of its own (host + gfx950 device code, registered with
-    # the HIP runtime when the library loads).
-    static_obj = os.path.join(BUILD, "rq_static.o")
-    _run([hipcc, "-c", "-fPIC", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_static.hip"), "-o", static_obj])
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     _run([
         "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",
-        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{CSRC}",
-        os.path.join(CSRC, "rq_host.cpp"), os.path.join(CSRC, "rq_gguf.cpp"), blob, static_obj,
+        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{csrc}",
+        os.path.join(csrc, "rq_host.cpp"), os.path.join(csrc, "rq_gguf.cpp"), blob, static_obj,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
         "-o", tmp,
     ])
-    os.replace(tmp, LIB)
-    # bench.py's read-floor probe (rq_floor.hip), a library of its own.
-    floor_tmp = FLOOR_LIB + ".tmp"
-    _run([hipcc, "-shared", "-fPIC", *HIPCC_FLAGS, f"-I{CSRC}", os.path.join(CSRC, "rq_floor.hip"), "-o", floor_tmp])
-    os.replace(floor_tmp, FLOOR_LIB)
+    os.replace(tmp, lib)
+    if floor:
+        os.replace(floor_lib + ".tmp", floor_lib)
     if verbose:
-        print(f"built {LIB} and {FLOOR_LIB}")
-    return LIB
+        print(f"built {lib}" + (f" and {floor_lib}" if floor else ""))
+    return lib
 
 
 if __name__ == "__main__":

@@ -243,6 +243,10 @@ struct rq_ctx {
     hipFunction_t mmqf[RQ_NUM_FMTS + 1][3] = {};
     hipFunction_t mmqd[RQ_NUM_FMTS][3][3] = {};
     hipFunction_t mmqg[RQ_NUM_FMTS + 1][2][3] = {};  // 8 x G columns, G = 2, 4
+    // 16 x G columns with four-activation entries (Q4_0, Q8_0, Q4_K; G = 1,
+    // 2, 4; sbw 2, 4), and the same classes of the fused gate/up (sbw 4)
+    hipFunction_t mmqt[RQ_NUM_FMTS][3][2] = {};
+    hipFunction_t mmqglut[RQ_NUM_FMTS][3] = {};
     // fused gate/up + activation (sbw 4): column classes 1, 4, 8, 8x2, 8x4; f32 x
     hipFunction_t mmqglu[RQ_NUM_FMTS][5] = {};
     hipFunction_t mmqgluf[RQ_NUM_FMTS] = {};
@@ -463,6 +467,9 @@ bool launch_compatible(const rq_weight* a, const rq_weight* b, int64_t m) {
     const bool ma = use_mmq(a, m);
     if (ma != use_mmq(b, m)) return false;
     if (a->type == b->type) return true;
+    // More than 8 MFMA columns run Q4_K in the 16-column classes, which Q6_K
+    // has not: a mixed launch would sum Q4_K in another order than its own.
+    if (ma && m > 8) return false;
     const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
     return ka && kb;
 }
@@ -589,28 +596,56 @@ bool mmq_supported(int fmt, int64_t cols) {
 }
 
 // Columns per launch: up to 8 in one staged group (mp = 1, 4, 8), or 8 x g
-// (g = 2, 4) staged one group after another against weights read once. (A
-// 64-column class lost to two 32-column launches except for Q8_0: each
-// workgroup stages all its columns for fewer rows, or the weights spill;
-// Q4_K 14336 x 4096: 61.7 or 117.6 us against 49.2.)
-constexpr int kMmqMaxCols = 32;
+// (g = 2, 4) staged one group after another against weights read once. Q4_0,
+// Q8_0 and Q4_K run more than 8 columns in the 16-column classes (mmqt_body:
+// four activations per lane entry), 16 columns staged per group, up to 64
+// per launch. (An 8-column class staging all 64 columns at once lost
+// to two 32-column launches except for Q8_0: each workgroup stages all its
+// columns for fewer rows, or the weights spill; Q4_K 14336 x 4096: 61.7 or
+// 117.6 us against 49.2.)
+bool mmq_has_t(int fmt, int S2) {
+    return (fmt == RQ_FMT_Q4_0 || fmt == RQ_FMT_Q8_0 || fmt == RQ_FMT_Q4_K) && (S2 + 3) / 4 <= 16;
+}
+int mmq_max_cols(int fmt, int S2) { return mmq_has_t(fmt, S2) ? 64 : 32; }
+// Group-count index of a 16-column class (g = 1, 2, 4).
+int mmqt_g_index(int g) { return g == 1 ? 0 : g == 2 ? 1 : 2; }
+// Super-blocks per wave of a 16-column launch: 4 for Q4_K; 2 for Q4_0 and
+// Q8_0, whose per-block scales (and Q8_0's 64 registers of codes at 4) would
+// not fit the 128 registers of a 1024-thread workgroup's waves with 4,
+// unless the row is too wide for 16 waves of 2.
+int mmqt_sbw(int fmt, int S2) { return fmt == RQ_FMT_Q4_K || (S2 + 1) / 2 > 16 ? 4 : 2; }
 
 struct MmqPlan {
-    int mp, g, sbw, ks, tr;
+    int mp, g, sbw, ks, tr;  // mp = 16: the 16-column classes
     int kxp, pl_off, part_off, lds;
 };
 
 // Kernel table index of a format (RQ_FMT_MIX_K: the mixed Q4_K / Q6_K kernels).
 int mmq_fi(int fmt) { return fmt == RQ_FMT_MIX_K ? RQ_NUM_FMTS : fmt; }
 
-hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, int mp, int g, int sbw, bool f32_in, bool dots) {
-    const int si = mmq_sbw_index(sbw), mi = mmq_mp_index(mp), fi = mmq_fi(fmt);
-    if (g > 1) return ctx->mmqg[fi][g == 2 ? 0 : 1][si];
+hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, const MmqPlan& L, bool f32_in, bool dots) {
+    if (L.mp == 16) {
+        if (L.sbw != 2 && L.sbw != 4) return nullptr;
+        return ctx->mmqt[fmt][mmqt_g_index(L.g)][L.sbw == 2 ? 0 : 1];
+    }
+    const int si = mmq_sbw_index(L.sbw), mi = mmq_mp_index(L.mp), fi = mmq_fi(fmt);
+    if (L.g > 1) return ctx->mmqg[fi][L.g == 2 ? 0 : 1][si];
     if (dots) return fmt == RQ_FMT_MIX_K ? nullptr : ctx->mmqd[fmt][mi][si];
     return f32_in ? ctx->mmqf[fi][si] : ctx->mmq[fi][mi][si];
 }
 
 void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
+    if (L.mp == 16) {
+        // 16 B of skew: the 16 lanes of one k-group read 16 B of each of the
+        // 16 columns in one instruction, which then fall in distinct 4-bank
+        // groups. Block-major planes (f16 scales, f32 f = dx sum q but for
+        // Q8_0); the partial sums of one group.
+        L.kxp = S2 * 256 + 16;
+        L.pl_off = 16 * L.kxp;
+        L.part_off = L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q8_0 ? 2 : 6);
+        L.lds = L.part_off + L.ks * L.tr * 64 * 4 * 4;
+        return;
+    }
     L.kxp = S2 * 256 + 64;  // 64 B of skew: columns start on different LDS banks
     L.pl_off = L.mp * L.kxp;
     L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * RQ_MMQ_NBP(S2) * 4;
@@ -636,20 +671,20 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
 // 16.1 / 26.2 us at 4 tiles per workgroup against 11.3 / 16.6 / 27.8 at 2;
 // Q4_K 4096 x 4096 6.3 / 9.5 / 16.0 at 1 against 9.1 / 14.2 / 24.4 at 4;
 // Q6_K 128256 x 4096 74 / 119 / 204 at 2 against 92 / 139 / 230 at 4.
-MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int g, int64_t tiles, bool f32_in, bool dots) {
-    MmqPlan L;
-    L.mp = mp;
-    L.g = g;
+MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t tiles, bool f32_in, bool dots) {
+    MmqPlan L = cls;
+    const int mp = L.mp;
     const int maxs = mmq_sbw_max(fmt);
     int sbw = 2;
     while (sbw < maxs && (S2 + sbw - 1) / sbw > 16) sbw *= 2;
     if (ctx->mmq_sbw >= sbw && ctx->mmq_sbw <= maxs && (ctx->mmq_sbw & (ctx->mmq_sbw - 1)) == 0)
         sbw = ctx->mmq_sbw;
-    else if (mp == 8 && !dots)
+    else if (mp >= 8 && !dots)
         sbw = std::max(sbw, std::min(4, maxs));
+    if (mp == 16) sbw = mmqt_sbw(fmt, S2);
     L.sbw = sbw;
     L.ks = (S2 + sbw - 1) / sbw;
-    if (ctx->mmq_tr > 0 || (mp == 8 && !dots)) {
+    if (ctx->mmq_tr > 0 || (mp >= 8 && !dots)) {
         const int tr_max = std::max(1, 16 / L.ks);
         if (ctx->mmq_tr > 0) {
             L.tr = std::min(ctx->mmq_tr, tr_max);
@@ -666,7 +701,7 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int g, int64_t tile
         }
         return L;
     }
-    hipFunction_t f = mmq_kernel(ctx, fmt, mp, g, sbw, f32_in, dots);
+    hipFunction_t f = mmq_kernel(ctx, fmt, L, f32_in, dots);
     int64_t best_rounds = -1;
     MmqPlan best = L;
     for (int tr = 1; tr * L.ks <= 16; tr *= 2) {
@@ -694,13 +729,20 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, int mp, int g, int64_t tile
 }
 
 
-// Column grouping of an MFMA launch of nc columns: mp (columns staged at
-// once: 1, 4 or 8) and g (groups of 8 staged in turn). Two columns run in
-// the 4-column class, whose shorter D-groups beat a 2-column class (Q4_K
-// 14336 x 4096: 8.40 against 9.76 us).
-void mmq_cols(int nc, int& mp, int& g) {
-    mp = nc <= 1 ? 1 : nc <= 4 ? 4 : 8;
-    g = nc <= 8 ? 1 : (nc <= 16 ? 2 : 4);
+// Column class of an MFMA launch of nc columns: mp (columns staged at once:
+// 1, 4, 8, or 16 for the 16-column classes) and g (groups staged in turn). Two
+// columns run in the 4-column class, whose shorter D-groups beat a 2-column
+// class (Q4_K 14336 x 4096: 8.40 against 9.76 us).
+MmqPlan mmq_cols(int fmt, int S2, int nc) {
+    MmqPlan L{};
+    if (nc > 8 && mmq_has_t(fmt, S2)) {
+        L.mp = 16;
+        L.g = nc <= 16 ? 1 : nc <= 32 ? 2 : 4;
+        return L;
+    }
+    L.mp = nc <= 1 ? 1 : nc <= 4 ? 4 : 8;
+    L.g = nc <= 8 ? 1 : (nc <= 16 ? 2 : 4);
+    return L;
 }
 
 // MFMA matvec / block-dot launches over `count` same-type weights of width k.
@@ -718,13 +760,11 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     const int S2 = ws[0]->S2;
     int64_t tiles = 0;
     for (int i = 0; i < count; i++) tiles += ws[i]->tiles;
-    const int max_cols = (xf || dots) ? (xf ? 1 : 8) : kMmqMaxCols;
+    const int max_cols = (xf || dots) ? (xf ? 1 : 8) : mmq_max_cols(fmt, S2);
     int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         const int nc = (int)((m + ngroups - 1) / ngroups);
-        int mp, g;
-        mmq_cols(nc, mp, g);
-        const MmqPlan L = mmq_plan(ctx, fmt, S2, mp, g, tiles, xf != nullptr, dots);
+        const MmqPlan L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
         if (L.lds <= ctx->lds_wide) break;
         if (nc == 1)
             return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage (%d bytes of LDS)", (long long)k, L.lds);
@@ -732,9 +772,7 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     }
     for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
         const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
-        int mp, g;
-        mmq_cols(nc, mp, g);
-        const MmqPlan P = mmq_plan(ctx, fmt, S2, mp, g, tiles, xf != nullptr, dots);
+        const MmqPlan P = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
         RqMmqParams p;
         memset(&p, 0, sizeof p);
         int64_t wgs = 0;
@@ -764,7 +802,7 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
         p.kxp = P.kxp;
         p.pl_off = P.pl_off;
         p.part_off = P.part_off;
-        hipFunction_t f = mmq_kernel(ctx, fmt, P.mp, P.g, P.sbw, xf != nullptr, dots);
+        hipFunction_t f = mmq_kernel(ctx, fmt, P, xf != nullptr, dots);
         if (!f) return fail(RQ_ERR_UNSUPPORTED, "matvec: no MFMA kernel for %d x %d columns, %d super-blocks per wave",
                             P.mp, P.g, P.sbw);
         rq_status st = launch(ctx, f, dots ? "rq_mmqd" : xf ? "rq_mmqf" : "rq_mmq", (uint64_t)wgs, &p, (unsigned)P.lds,
@@ -793,15 +831,20 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
     const int fmt = gate->fmt, S2 = gate->S2;
     const int64_t k = gate->cols, n = gate->rows, U = k / 32;
     auto plan = [&](int nc, MmqPlan& L, int& h_off) {
-        mmq_cols(nc, L.mp, L.g);
+        L = mmq_cols(fmt, S2, nc);
         L.sbw = 4;
         L.ks = (S2 + 3) / 4;
         L.tr = 2;
         mmq_layout(fmt, S2, false, L);
-        h_off = L.part_off + 2 * L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4;  // both weights' partials
-        L.lds = h_off + L.g * L.mp * 32 * 4;
+        if (L.mp == 16) {  // both weights' partials of one group; h of one group
+            h_off = L.part_off + 2 * L.ks * L.tr * 64 * 4 * 4;
+            L.lds = h_off + 16 * 32 * 4;
+        } else {
+            h_off = L.part_off + 2 * L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4;  // both weights' partials
+            L.lds = h_off + L.g * L.mp * 32 * 4;
+        }
     };
-    const int max_cols = xf ? 1 : kMmqMaxCols;
+    const int max_cols = xf ? 1 : mmq_max_cols(fmt, S2);
     int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         MmqPlan L;
@@ -848,7 +891,9 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
         p.hs = hq ? hs + g0 * n / 32 : nullptr;
         p.act = act;
         const int cls = L.g > 1 ? (L.g == 2 ? 3 : 4) : mmq_mp_index(L.mp);
-        hipFunction_t f = xf ? ctx->mmqgluf[fmt] : ctx->mmqglu[fmt][cls];
+        hipFunction_t f = xf     ? ctx->mmqgluf[fmt]
+                          : L.mp == 16 ? ctx->mmqglut[fmt][mmqt_g_index(L.g)]
+                                 : ctx->mmqglu[fmt][cls];
         rq_status st = launch(ctx, f, xf ? "rq_mmqgluf" : "rq_mmqglu", (uint64_t)(gate->tiles / 2), &p,
                               (unsigned)L.lds, (unsigned)(64 * 2 * L.ks * L.tr));
         if (st != RQ_OK) return st;
@@ -1045,6 +1090,17 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
                 snprintf(name, sizeof name, "rq_mmqd_%s_%d_%d", kFmtSuffix[f], kMmqMp[mi], kMmqSbw[si]);
                 st = getm(ctx->mmq_mod, &ctx->mmqd[f][mi][si], name);
             }
+        }
+    }
+    for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
+        if (f == RQ_FMT_Q6_K) continue;  // no 16-column classes
+        for (int gi = 0; gi < 3 && st == RQ_OK; gi++) {
+            for (int si = 0; si < 2 && st == RQ_OK; si++) {
+                snprintf(name, sizeof name, "rq_mmq_%s_16x%d_%d", kFmtSuffix[f], 1 << gi, kMmqSbw[si]);
+                st = getm(ctx->mmq_mod, &ctx->mmqt[f][gi][si], name);
+            }
+            snprintf(name, sizeof name, "rq_mmqglu_%s_16x%d", kFmtSuffix[f], 1 << gi);
+            if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmqglut[f][gi], name);
         }
     }
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
@@ -1471,7 +1527,9 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matvec: output %d not 4-byte aligned", i);
         if (use_mmq(ws[i], m) != use_mmq(ws[0], m))
             return fail(RQ_ERR_SHAPE, "matvec: weights laid out for different kernel families in one launch");
-        if (!launch_compatible(ws[0], ws[i], m))
+        const bool kq = (ws[0]->fmt == RQ_FMT_Q4_K || ws[0]->fmt == RQ_FMT_Q6_K) &&
+                        (ws[i]->fmt == RQ_FMT_Q4_K || ws[i]->fmt == RQ_FMT_Q6_K);
+        if (ws[i]->type != ws[0]->type && !kq)
             return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
                         type_name(ws[i]->type));
         if (ws[i]->cols != ws[0]->cols)
@@ -1485,7 +1543,23 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if ((st = check_len("matmul out", out_lens[i], m * ws[i]->rows)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
-    if (use_mmq(ws[0], m)) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
+    if (use_mmq(ws[0], m)) {
+        bool one = true;  // Q4_K with Q6_K past 8 columns: a launch per type (launch_compatible)
+        for (int i = 1; i < count; i++) one = one && launch_compatible(ws[0], ws[i], m);
+        if (one) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
+        for (int f : {RQ_FMT_Q4_K, RQ_FMT_Q6_K}) {
+            const rq_weight* sw[RQ_MV_TARGETS];
+            void* so[RQ_MV_TARGETS];
+            int c = 0;
+            for (int i = 0; i < count; i++)
+                if (ws[i]->fmt == f) {
+                    sw[c] = ws[i];
+                    so[c++] = outs[i];
+                }
+            if (c && (st = mmq_launch(ctx, xq->qs, xq->d, nullptr, m, sw, so, c, false)) != RQ_OK) return st;
+        }
+        return RQ_OK;
+    }
     return matvec_launch(ctx, xq->qs, xq->d, nullptr, m, ws, outs, count);
 }
 

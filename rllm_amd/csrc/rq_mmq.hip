@@ -106,6 +106,20 @@ __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b,
     if (DOTS) *(int*)(pl + NPL * stride) = sq;
 }
 
+// The 16-column classes (mmqt_body) keep their planes block-major: the f16
+// activation scale dx of block b, column a at pl_off + ((b / 2) * 16 + a) *
+// 4 + (b % 2) * 2 (a lane reads four columns' scales of both blocks of a
+// window in 16 bytes), and, except for Q8_0, f = dx sum q as f32 at
+// pl_off + 8 * S2 * 16 * 2 + (b * 16 + a) * 4 (consecutive columns: the
+// correction MFMA's A operand).
+template <int FMT>
+__device__ __forceinline__ void stage_planes_t(const RqMmqParams& P, int a, int b, int sq, u32 d16) {
+    char* pl = mmq_lds + P.pl_off;
+    *(u16*)(pl + ((b >> 1) * 16 + a) * 4 + (b & 1) * 2) = (u16)d16;
+    if (FMT != RQ_FMT_Q8_0)
+        ((float*)(pl + 8 * P.S2 * 16 * 2))[b * 16 + a] = h2f(d16) * (float)sq;  // exact: f16 times |sq| <= 4064
+}
+
 // One Q8_1 block (codes and f16 scale) in registers. The loads are
 // unconditional (from a clamped, valid address) and `valid` zeroes the block
 // when it is written: a guarded load would let the compiler consume its value
@@ -126,7 +140,7 @@ __device__ __forceinline__ void xb_load(const RqMmqParams& P, int a, int b, XB& 
     x.d16 = P.xd[(int64_t)ac * U + bc];
 }
 
-template <int FMT, int MP, bool DOTS>
+template <int FMT, int MP, bool DOTS, bool TP = false>
 __device__ __forceinline__ void xb_write(const RqMmqParams& P, int a, int b, XB x) {
     if (!x.valid) {
         x.lo = make_int4(0, 0, 0, 0);
@@ -145,7 +159,10 @@ __device__ __forceinline__ void xb_write(const RqMmqParams& P, int a, int b, XB 
     char* xp = mmq_lds + a * P.kxp + b * 32;
     *(int4*)xp = x.lo;
     *(int4*)(xp + 16) = x.hi;
-    stage_planes<FMT, MP, DOTS>(P, a, b, sq, h2f(x.d16));
+    if constexpr (TP)
+        stage_planes_t<FMT>(P, a, b, sq, x.d16);
+    else
+        stage_planes<FMT, MP, DOTS>(P, a, b, sq, h2f(x.d16));
 }
 
 // f32 staging of one column (rq_mmqf_*): four lanes (a quad) per block, eight
@@ -655,6 +672,281 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-column groups with four activations per lane entry
+// (rq_mmq_<fmt>_16x<g>_<sbw>: up to 16 g columns per launch, staged 16 at a
+// time against weights read once into registers). A D entry is the exact
+// int32 dot of one 32-element block of the lane's weight row n with one
+// activation. The A operand's rows are the group's 16 activations, one
+// 16-byte LDS read per lane and window (all lanes: k-group g of activation
+// lane % 16); each window takes two MFMAs, one per block h, whose B operand
+// is the weight window with the other block's k-groups zeroed (a lane mask
+// folded into the nibble mask). Lane (g, n)'s entries are then block 2w + h,
+// activations 4g .. 4g + 3: the row's scales serve all four, and their
+// activation scales are one 16-byte LDS read per window (f16, both blocks).
+// Per entry the scaling is three VALU instructions: sc * D in int32 (Q4_K;
+// |sc D| < 2^26), its f32, one fma with the f16 activation scale. The
+// high windows' factor 16 (XOR-8 codes masked with 0xF0) is taken out once
+// per super-block: their entries accumulate apart and join scaled by 1/16.
+//
+// Terms that do not depend on the codes (Q4_K: the min term and the 8 sum x
+// of the high windows' XOR-8 codes; Q4_0: the -8 sum x of the low windows)
+// are, per (activation a, row r), sum_b f(a, b) c(b, r) over the blocks b of
+// the k-part, with f = dx sum q from the staging and c from the row's
+// header: an f32 product of a [16 x blocks] by a [blocks x 16] matrix, one
+// v_mfma_f32_16x16x4_f32 per half super-block, whose D entries are the int8
+// MFMAs' (activation, row) pairs.
+//   Q4_K  c(b, r) = 8 d sc_b [b in a high window] - dmin m_b
+//   Q4_0  c(b, r) = -8 d_b [b in a low window]
+// After each group the k-parts' sums meet in LDS (a fixed order) and are
+// stored (or, with GLU, become h = act(g) u and its Q8_1), so LDS holds the
+// partial sums of one group only.
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+
+// Byte i (lane-varying) of a dword.
+__device__ __forceinline__ u32 vbyte(u32 w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// f32 of the f16 in half h (0 = low) of a dword.
+__device__ __forceinline__ float hsel(u32 w, int h) { return (float)__builtin_bit_cast(_Float16, (u16)(w >> (16 * h))); }
+
+// Partial sum of activation a (of the group), tile row nn, left by wave slot w.
+__device__ __forceinline__ float partt_at(const float* part, int w, int a, int nn) {
+    return part[(w * 64 + 16 * (a >> 2) + nn) * 4 + (a & 3)];
+}
+
+// The first two rounds of column group gi's staging loads (items tid and
+// tid + threads), issued ahead: group 0's before the weight loads (a staging
+// load issued after them could only be waited for together with every weight
+// load, vmcnt retiring in order), each later group's before the arithmetic
+// of the group before it, so that its latency is hidden.
+__device__ __forceinline__ void mmqt_prefetch(const RqMmqParams& P, int gi, XB& x0, XB& x1) {
+    const int threads = blockDim.x, tid = threadIdx.x;
+    xb_load(P, gi * 16 + (tid & 15), tid >> 4, x0);
+    xb_load(P, gi * 16 + ((tid + threads) & 15), (tid + threads) >> 4, x1);
+}
+
+// Staging of column group gi between barriers, from its prefetched rounds.
+template <int FMT>
+__device__ __forceinline__ void mmqt_stage(const RqMmqParams& P, int gi, const XB& x0, const XB& x1) {
+    const int threads = blockDim.x, tid = threadIdx.x, items = 16 * 8 * P.S2;
+    if (gi > 0) __syncthreads();  // the previous group's LDS reads are done
+    int it = tid;
+    if (it < items) xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x0);
+    it += threads;
+    if (it < items) xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x1);
+    it += threads;
+    for (; it < items; it += threads) {
+        XB x;
+        xb_load(P, gi * 16 + (it & 15), it >> 4, x);
+        xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x);
+    }
+    __syncthreads();
+}
+
+template <int FMT, int SBW, int G, bool GLU>
+__device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
+    constexpr bool NIB = MF<FMT>::NIB;
+    constexpr int LPS = NIB ? 2 : 4;  // code loads per super-block
+    constexpr int NLD = LPS * SBW;
+
+    const int tid = threadIdx.x, threads = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+
+    const int blk = blockIdx.x;
+    int ti = 0, wtl = wave;  // wtl: the wave within its target's waves
+    if (GLU) {  // gate's waves, then up's, on the same tiles
+        ti = wave >= P.ks * P.tr ? 1 : 0;
+        wtl = wave - ti * P.ks * P.tr;
+    } else {
+        if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
+        if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    }
+    const RqMmqTarget T = pick_target(P, ti);
+    const int ks = P.ks;
+    const int tl = wtl / ks, kpart = wtl - (wtl / ks) * ks;
+    const int tile = (blk - T.wg_start) * P.tr + tl;
+    const bool has_tile = tile < T.tiles;  // wave-uniform
+    const int tile_c = has_tile ? tile : T.tiles - 1;
+    const int S2 = P.S2, NB = 8 * S2;
+    const int sb0 = kpart * SBW;           // first super-block of the part
+    const int nsb = min(SBW, S2 - sb0);    // even, >= 2
+
+    // ---- Group 0's staging loads, then every weight load of the wave: per
+    // super-block the lane's header (row n) and its code loads.
+    XB x0, x1;
+    mmqt_prefetch(P, 0, x0, x1);  // item it = 16 * block + column
+    int4 wv[NLD];
+    int4 hv[SBW];
+    const u8* cb = T.code + ((int64_t)tile_c * LPS * S2 + (int64_t)sb0 * LPS) * 1024 + lane * 16;
+    const u8* hb = T.hdr + ((int64_t)tile_c * S2 + sb0) * 256 + n * 16;
+    // Super-block i's loads: its header, then its codes.
+    auto load_sb = [&](int i) {
+        hv[i] = ld16_nt(hb + min(i, nsb - 1) * 256);
+#pragma unroll
+        for (int j = 0; j < LPS; j++) wv[i * LPS + j] = ld16_nt(cb + (int64_t)min(i * LPS + j, nsb * LPS - 1) * 1024);
+    };
+    // The first super-block's loads go out now, each later one's while group
+    // 0 computes the one before it: issued all at once, the loads of the
+    // workgroup's 16 waves stalled each wave's issue until most of its data
+    // was in, and no arithmetic overlapped them (Q4_K 14336 x 4096 at 16 /
+    // 32 / 64 columns: 13.4 / 20.4 / 36.6 -> 12.3 / 19.5 / 34.7 us; a
+    // pipeline two super-blocks deep was in between).
+    constexpr int PRE = 1;
+#pragma unroll
+    for (int i = 0; i < PRE; i++) load_sb(i);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Per super-block, decoded at group 0 and kept for the later groups:
+    // Q4_K the two scale words and d (q4k_decode); the correction operand c
+    // of the lane's row and block 4 hf + g (hf = 0, 1).
+    u32 ksc[SBW][2];
+    float kd[SBW];
+    float cb4[SBW][2];
+    // B masks of MFMA h: the nibble (or byte) mask where the lane's k-group
+    // lies in block h, else 0 (mk[window parity][h]).
+    u32 mk[2][2];
+#pragma unroll
+    for (int par = 0; par < 2; par++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const u32 m = NIB ? (par ? 0xF0F0F0F0u : 0x0F0F0F0Fu) : 0xFFFFFFFFu;
+            mk[par][h] = (g >> 1) == h ? m : 0u;
+        }
+
+    const char* dxp = mmq_lds + P.pl_off;                          // f16 dx, [block pair][16][2]
+    const float* fpl = (const float*)(mmq_lds + P.pl_off + NB * 16 * 2);  // f32 f, [block][16]
+    float* part = (float*)(mmq_lds + P.part_off);
+    const int ia = lane & 15;  // A row: activation ia
+
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+    mmqt_stage<FMT>(P, gi, x0, x1);
+    if (gi + 1 < G) mmqt_prefetch(P, gi + 1, x0, x1);
+    v4f y = {0.f, 0.f, 0.f, 0.f};
+
+    if (has_tile) {
+        const int xoff = ia * P.kxp + sb0 * 256 + 16 * g;
+        v4f C = {0.f, 0.f, 0.f, 0.f};  // the correction product (Q4_K, Q4_0)
+#pragma unroll
+        for (int i = 0; i < SBW; i++) {
+            if (i >= nsb) break;  // a short last k-part (uniform)
+            const int b0 = (sb0 + i) * 8;  // first block of the super-block
+            if (gi == 0 && i + PRE < SBW) {
+                load_sb(i + PRE);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (gi == 0) {
+                if (FMT == RQ_FMT_Q4_K) {
+                    u32 kq[4];
+                    float kf[2];
+                    q4k_decode(hv[i], kq, kf);
+                    ksc[i][0] = kq[0];
+                    ksc[i][1] = kq[2];
+                    kd[i] = kf[0];
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        const float scf = (float)vbyte(kq[2 * hf], g), mf = (float)vbyte(kq[2 * hf + 1], g);
+                        const float hi8d = ((g >> 1) & 1) ? 8.f * kf[0] : 0.f;
+                        cb4[i][hf] = fmaf(hi8d, scf, -kf[1] * mf);
+                    }
+                } else if (FMT == RQ_FMT_Q4_0) {
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) {
+                        const u32 wd = (u32)(hf == 0 ? (g < 2 ? hv[i].x : hv[i].y) : (g < 2 ? hv[i].z : hv[i].w));
+                        const float db = half_f(wd, g & 1);
+                        cb4[i][hf] = ((g >> 1) & 1) ? 0.f : -8.f * db;
+                    }
+                }
+            }
+            // Entries of the low windows (0, 2) and the high ones (1, 3).
+            v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const int4 v = NIB ? wv[i * 2 + (w >> 1)] : wv[i * 4 + w];
+                const v4i A = lds16(xoff + 256 * i + 64 * w);
+                // dx of activations a4 .. a4 + 3 (dwords), blocks 2w (low halves) and 2w + 1
+                const int4 dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const u32 m = mk[NIB ? (w & 1) : 0][h];
+                    const v4i B = v4i{(int)((u32)v.x & m), (int)((u32)v.y & m), (int)((u32)v.z & m), (int)((u32)v.w & m)};
+                    const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i{0, 0, 0, 0}), 0, 0, 0);
+                    const u32 dxv[4] = {(u32)dxw.x, (u32)dxw.y, (u32)dxw.z, (u32)dxw.w};
+                    const int b = 2 * w + h;  // block within the super-block
+                    v4f& ac = acc[NIB ? (w & 1) : 0];
+                    if (FMT == RQ_FMT_Q4_K) {
+                        const int sc = (int)vbyte(ksc[i][w >> 1], b & 3);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)__mul24(sc, D[e]), hsel(dxv[e], h), ac[e]);
+                    } else {
+                        const u32 wd = (u32)(w == 0 ? hv[i].x : w == 1 ? hv[i].y : w == 2 ? hv[i].z : hv[i].w);
+                        const float db = half_f(wd, h);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)D[e] * hsel(dxv[e], h), db, ac[e]);
+                    }
+                }
+            }
+            const float s0 = FMT == RQ_FMT_Q4_K ? kd[i] : 1.f;
+            y += s0 * acc[0];
+            if (NIB) y += (0.0625f * s0) * acc[1];
+            if (FMT != RQ_FMT_Q8_0) {
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const float fa = fpl[(b0 + 4 * hf + g) * 16 + ia];
+                    C = __builtin_amdgcn_mfma_f32_16x16x4f32(fa, cb4[i][hf], C, 0, 0, 0);
+                }
+            }
+        }
+        y += C;
+    }
+    // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
+    *(v4f*)(part + (wave * 64 + lane) * 4) = y;
+    __syncthreads();
+    if (!GLU) {
+        float* out = (float*)T.out;
+        for (int it = tid; it < P.tr * 256; it += threads) {
+            const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15;
+            const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn, ag = gi * 16 + a;
+            if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
+            float s = 0.f;
+            for (int q = 0; q < ks; q++) s += partt_at(part, tl2 * ks + q, a, nn);
+            gmem(out)[(int64_t)ag * T.n + row] = s;
+        }
+    } else {
+        const int kt = ks * P.tr;
+        float* hl = (float*)(mmq_lds + P.h_off);  // [16][32]
+        for (int it = tid; it < P.tr * 256; it += threads) {
+            const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15, ag = gi * 16 + a;
+            float gs = 0.f, us = 0.f;
+            for (int q = 0; q < ks; q++) {
+                gs += partt_at(part, tl2 * ks + q, a, nn);
+                us += partt_at(part, kt + tl2 * ks + q, a, nn);
+            }
+            const float h = act_apply(P.act, gs) * us;
+            const int row = (blk * P.tr + tl2) * 16 + nn;
+            if (P.hf && ag < P.m) gmem(P.hf)[(int64_t)ag * T.n + row] = h;
+            hl[a * 32 + tl2 * 16 + nn] = h;
+        }
+        if (P.hq) {  // uniform
+            __syncthreads();
+            for (int base = 0; base < 16 * 8; base += threads) {  // uniform trip count: whole 8-lane groups
+                const int t = base + tid;
+                const bool in = t < 16 * 8;
+                const int a = in ? t >> 3 : 0, f4 = t & 7, ag = gi * 16 + a;
+                float h[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) h[j] = hl[a * 32 + 4 * f4 + j];
+                q8_emit4(h, ((int64_t)ag * T.n + blk * 32) / 4 + f4, in && ag < P.m, P.hq, P.hd, P.hs);
+            }
+        }
+    }
+    }  // column groups
+}
+
+// ---------------------------------------------------------------------------
 // Q6_K. Its sub-blocks are 16 elements (one k-group), each with its own int8
 // scale, so an A row covers one k-group of one window instead of a
 // 32-element block:
@@ -971,6 +1263,26 @@ RQ_MMQ_GLU_SET(q4_0, RQ_FMT_Q4_0)
 RQ_MMQ_GLU_SET(q8_0, RQ_FMT_Q8_0)
 RQ_MMQ_GLU_SET(q4_k, RQ_FMT_Q4_K)
 RQ_MMQ_GLU_SET(q6_k, RQ_FMT_Q6_K)
+
+// 16 x g columns (Q4_0, Q8_0, Q4_K; sbw 2, 4) and the fused gate/up of the
+// same classes (sbw 4).
+#define RQ_MMQT(NAME, FMT, G, SBW)                                                                         \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_##NAME##_16x##G##_##SBW(RqMmqParams p) {       \
+        mmqt_body<FMT, SBW, G, false>(p);                                                                   \
+    }
+#define RQ_MMQT_SET(NAME, FMT, G)                                                                          \
+    RQ_MMQT(NAME, FMT, G, 2)                                                                               \
+    RQ_MMQT(NAME, FMT, G, 4)                                                                               \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_16x##G(RqMmqParams p) {           \
+        mmqt_body<FMT, 4, G, true>(p);                                                                      \
+    }
+#define RQ_MMQT_FMT(NAME, FMT)                                                                             \
+    RQ_MMQT_SET(NAME, FMT, 1)                                                                              \
+    RQ_MMQT_SET(NAME, FMT, 2)                                                                              \
+    RQ_MMQT_SET(NAME, FMT, 4)
+RQ_MMQT_FMT(q4_0, RQ_FMT_Q4_0)
+RQ_MMQT_FMT(q8_0, RQ_FMT_Q8_0)
+RQ_MMQT_FMT(q4_k, RQ_FMT_Q4_K)
 
 // Mixed Q4_K / Q6_K launches (no block-dot variants: those run per weight).
 #define RQ_MMQ_MIX(MP, SBW)                                                                          \

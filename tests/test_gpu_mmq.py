@@ -1,7 +1,8 @@
 """GPU parity of the int8-MFMA kernels (rq_mmq.hip) through the C-ABI.
 
 The MFMA kernels split the activation columns into classes of 1, 4 or 8
-per launch (and 8 x 2, 8 x 4), stage k in super-block parts of 2, 4 or 8 per
+per launch (and 8 x 2, 8 x 4; Q4_0, Q8_0 and Q4_K run 9 to 64 columns as
+16 x 1, 16 x 2, 16 x 4), stage k in super-block parts of 2, 4 or 8 per
 wave, pad k to an even number of 256-element super-blocks and rows to tiles
 of 16; Q6_K has its own D-group shapes (16-element sub-blocks). These tests
 walk those cases against the CPU oracle (block dots bit-exact, f32 outputs
@@ -44,15 +45,16 @@ def _run(gpu, orc, t, n, k, m, seed, kind="random", dots=True):
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 32, 33])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 32, 33, 48, 64, 65])
 def test_mmq_column_classes(mfma, orc, tname, m):
-    """Every column class (1, 2, 4, 8 per launch), padded classes and several launches."""
+    """Every column class (1, 4, 8 per launch; 8 x 2, 8 x 4; 16 x 1, 16 x 2,
+    16 x 4), padded classes and several launches."""
     _run(mfma, orc, MMQ_TYPES[tname], 45, 1024, m, 300 + m)
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
 @pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480])
-@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("m", [1, 3, 8, 20])
 def test_mmq_widths(mfma, orc, tname, k, m):
     """Odd super-block counts (zero padding to an even count), 2/4/8 super-blocks per wave."""
     t = MMQ_TYPES[tname]
