@@ -108,13 +108,14 @@ struct SB {
     u32 tail;  // Q6_K: f16 d
 };
 
-// WAVE_ORDER: an s_barrier after each chunk load but the last, so that the
-// workgroup's waves request chunk c of their tiles before any requests chunk
-// c + 1. Issued wave by wave, one wave's chunks came back together and the
+// WAVE_ORDER: an s_barrier after each of the first eight chunk loads (but
+// the last), so that the workgroup's waves request chunk c of their tiles
+// before any requests chunk c + 1. Issued wave by wave, one wave's chunks came back together and the
 // whole of its arithmetic followed the last of them; interleaved, each wave's
 // chunks arrive spread out and little of its work is left after its last one
 // (one column, Q4_K 14336 x 4096: 7.26 -> 7.16 us; 4096 x 4096: 3.98 ->
-// 3.83 us). Every wave of the workgroup must make the call.
+// 3.83 us; Q6_K 4096 x 14336: 9.82 -> 9.64 us; Q8_0 gained nothing). Every
+// wave of the workgroup must make the call.
 template <int FMT, bool WAVE_ORDER = false>
 __device__ __forceinline__ void load_sb(const RqTiled& w, int t, int a, SB<FMT>& o) {
     constexpr int C = Fmt<FMT>::C;
@@ -123,7 +124,7 @@ __device__ __forceinline__ void load_sb(const RqTiled& w, int t, int a, SB<FMT>&
 #pragma unroll
     for (int c = 0; c < C; c++) {
         o.c[c] = ld16_nt(base + (int64_t)c * slots * 16);
-        if (WAVE_ORDER && c < C - 1) {
+        if (WAVE_ORDER && c < 8 && c < C - 1) {
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
@@ -680,7 +681,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
 
     // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
-    constexpr bool ORDER = NC == 1 && !KP && (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0);
+    constexpr bool ORDER = NC == 1 && !KP && FMT != RQ_FMT_Q8_0;
     stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
     if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
 
