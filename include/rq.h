@@ -169,7 +169,7 @@ rq_status rq_matvec(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* 
  * mixed (q/k/v of a Q4_K_M file), and run by one kernel family at this m
  * (a dot4 weight with an MFMA one fails with RQ_ERR_SHAPE). A Q4_K / Q6_K
  * mix on MFMA weights over more than 8 columns runs as one launch per type
- * (Q4_K's 16-column kernels have no Q6_K form), so each output is
+ * (the 16-column kernels have no mixed form), so each output is
  * bit-identical to the weight's own rq_matvec. out_lens[i] >= m * rows_i. */
 rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* const* ws, float* const* outs,
                          const int64_t* out_lens, int count);

@@ -467,8 +467,8 @@ bool launch_compatible(const rq_weight* a, const rq_weight* b, int64_t m) {
     const bool ma = use_mmq(a, m);
     if (ma != use_mmq(b, m)) return false;
     if (a->type == b->type) return true;
-    // More than 8 MFMA columns run Q4_K in the 16-column classes, which Q6_K
-    // has not: a mixed launch would sum Q4_K in another order than its own.
+    // More than 8 MFMA columns run each type in its 16-column classes, which
+    // have no mixed form: a mixed launch would sum in another order.
     if (ma && m > 8) return false;
     const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
     return ka && kb;
@@ -603,17 +603,18 @@ bool mmq_supported(int fmt, int64_t cols) {
 // to two 32-column launches except for Q8_0: each workgroup stages all its
 // columns for fewer rows, or the weights spill; Q4_K 14336 x 4096: 61.7 or
 // 117.6 us against 49.2.)
-bool mmq_has_t(int fmt, int S2) {
-    return (fmt == RQ_FMT_Q4_0 || fmt == RQ_FMT_Q8_0 || fmt == RQ_FMT_Q4_K) && (S2 + 3) / 4 <= 16;
-}
-int mmq_max_cols(int fmt, int S2) { return mmq_has_t(fmt, S2) ? 64 : 32; }
+bool mmq_has_t(int fmt, int S2) { return fmt != RQ_FMT_MIX_K && (S2 + 3) / 4 <= 16; }
+// Q6_K runs the 16-column kernels for up to 16 columns only: holding its
+// weights for a second group makes them spill.
+int mmqt_max_cols(int fmt) { return fmt == RQ_FMT_Q6_K ? 16 : 64; }
+int mmq_max_cols(int fmt, int S2) { return mmq_has_t(fmt, S2) && fmt != RQ_FMT_Q6_K ? 64 : 32; }
 // Group-count index of a 16-column class (g = 1, 2, 4).
 int mmqt_g_index(int g) { return g == 1 ? 0 : g == 2 ? 1 : 2; }
 // Super-blocks per wave of a 16-column launch: 4 for Q4_K; 2 for Q4_0 and
 // Q8_0, whose per-block scales (and Q8_0's 64 registers of codes at 4) would
 // not fit the 128 registers of a 1024-thread workgroup's waves with 4,
 // unless the row is too wide for 16 waves of 2.
-int mmqt_sbw(int fmt, int S2) { return fmt == RQ_FMT_Q4_K || (S2 + 1) / 2 > 16 ? 4 : 2; }
+int mmqt_sbw(int fmt, int S2) { return fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q6_K || (S2 + 1) / 2 > 16 ? 4 : 2; }
 
 struct MmqPlan {
     int mp, g, sbw, ks, tr;  // mp = 16: the 16-column classes
@@ -642,7 +643,7 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
         // Q8_0); the partial sums of one group.
         L.kxp = S2 * 256 + 16;
         L.pl_off = 16 * L.kxp;
-        L.part_off = L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q8_0 ? 2 : 6);
+        L.part_off = L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q4_0 ? 6 : 2);
         L.lds = L.part_off + L.ks * L.tr * 64 * 4 * 4;
         return;
     }
@@ -733,9 +734,9 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
 // 1, 4, 8, or 16 for the 16-column classes) and g (groups staged in turn). Two
 // columns run in the 4-column class, whose shorter D-groups beat a 2-column
 // class (Q4_K 14336 x 4096: 8.40 against 9.76 us).
-MmqPlan mmq_cols(int fmt, int S2, int nc) {
+MmqPlan mmq_cols(int fmt, int S2, int nc, bool allow16 = true) {
     MmqPlan L{};
-    if (nc > 8 && mmq_has_t(fmt, S2)) {
+    if (allow16 && nc > 8 && nc <= mmqt_max_cols(fmt) && mmq_has_t(fmt, S2)) {
         L.mp = 16;
         L.g = nc <= 16 ? 1 : nc <= 32 ? 2 : 4;
         return L;
@@ -760,19 +761,27 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     const int S2 = ws[0]->S2;
     int64_t tiles = 0;
     for (int i = 0; i < count; i++) tiles += ws[i]->tiles;
+    // The plan of a launch of nc columns: the 16-column classes where they
+    // apply and their staging fits, else the 8-column ones (up to 32).
+    auto plan_for = [&](int nc) {
+        MmqPlan L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
+        if (L.mp == 16 && L.lds > ctx->lds_wide)
+            L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc, false), tiles, xf != nullptr, dots);
+        return L;
+    };
     const int max_cols = (xf || dots) ? (xf ? 1 : 8) : mmq_max_cols(fmt, S2);
     int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         const int nc = (int)((m + ngroups - 1) / ngroups);
-        const MmqPlan L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
-        if (L.lds <= ctx->lds_wide) break;
+        const MmqPlan L = plan_for(nc);
+        if (L.lds <= ctx->lds_wide && (L.mp == 16 || nc <= 32)) break;
         if (nc == 1)
             return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage (%d bytes of LDS)", (long long)k, L.lds);
         ngroups++;
     }
     for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
         const int nc = (int)(m / ngroups + (gi < m % ngroups ? 1 : 0));
-        const MmqPlan P = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
+        const MmqPlan P = plan_for(nc);
         RqMmqParams p;
         memset(&p, 0, sizeof p);
         int64_t wgs = 0;
@@ -831,7 +840,10 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
     const int fmt = gate->fmt, S2 = gate->S2;
     const int64_t k = gate->cols, n = gate->rows, U = k / 32;
     auto plan = [&](int nc, MmqPlan& L, int& h_off) {
-        L = mmq_cols(fmt, S2, nc);
+        // The 16-column classes at 4 super-blocks per wave hold their weights
+        // across groups without spilling only for Q4_K up to two groups and
+        // for every type at one.
+        L = mmq_cols(fmt, S2, nc, nc <= (fmt == RQ_FMT_Q4_K ? 32 : 16));
         L.sbw = 4;
         L.ks = (S2 + 3) / 4;
         L.tr = 2;
@@ -844,7 +856,7 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
             L.lds = h_off + L.g * L.mp * 32 * 4;
         }
     };
-    const int max_cols = xf ? 1 : mmq_max_cols(fmt, S2);
+    const int max_cols = xf ? 1 : 32;  // the classes above take at most 32
     int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         MmqPlan L;
@@ -1093,9 +1105,8 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
         }
     }
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
-        if (f == RQ_FMT_Q6_K) continue;  // no 16-column classes
-        for (int gi = 0; gi < 3 && st == RQ_OK; gi++) {
-            for (int si = 0; si < 2 && st == RQ_OK; si++) {
+        for (int gi = 0; gi < (f == RQ_FMT_Q6_K ? 1 : 3) && st == RQ_OK; gi++) {  // Q6_K: 16 x 1, sbw 4 only
+            for (int si = f == RQ_FMT_Q6_K ? 1 : 0; si < 2 && st == RQ_OK; si++) {
                 snprintf(name, sizeof name, "rq_mmq_%s_16x%d_%d", kFmtSuffix[f], 1 << gi, kMmqSbw[si]);
                 st = getm(ctx->mmq_mod, &ctx->mmqt[f][gi][si], name);
             }

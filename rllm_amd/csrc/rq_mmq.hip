@@ -109,14 +109,14 @@ __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b,
 // The 16-column classes (mmqt_body) keep their planes block-major: the f16
 // activation scale dx of block b, column a at pl_off + ((b / 2) * 16 + a) *
 // 4 + (b % 2) * 2 (a lane reads four columns' scales of both blocks of a
-// window in 16 bytes), and, except for Q8_0, f = dx sum q as f32 at
+// window in 16 bytes), and, for Q4_K and Q4_0, f = dx sum q as f32 at
 // pl_off + 8 * S2 * 16 * 2 + (b * 16 + a) * 4 (consecutive columns: the
 // correction MFMA's A operand).
 template <int FMT>
 __device__ __forceinline__ void stage_planes_t(const RqMmqParams& P, int a, int b, int sq, u32 d16) {
     char* pl = mmq_lds + P.pl_off;
     *(u16*)(pl + ((b >> 1) * 16 + a) * 4 + (b & 1) * 2) = (u16)d16;
-    if (FMT != RQ_FMT_Q8_0)
+    if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0)
         ((float*)(pl + 8 * P.S2 * 16 * 2))[b * 16 + a] = h2f(d16) * (float)sq;  // exact: f16 times |sq| <= 4064
 }
 
@@ -747,6 +747,52 @@ __device__ __forceinline__ void mmqt_stage(const RqMmqParams& P, int gi, const X
     __syncthreads();
 }
 
+// Column group gi's sums over the ks k-parts of the workgroup's tiles, in
+// a fixed order, stored as out[a * n + row].
+__device__ __forceinline__ void mmqt_reduce(const RqMmqParams& P, const RqMmqTarget& T, int gi, const float* part) {
+    const int threads = blockDim.x, tid = threadIdx.x, blk = blockIdx.x, ks = P.ks;
+    float* out = (float*)T.out;
+    for (int it = tid; it < P.tr * 256; it += threads) {
+        const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15;
+        const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn, ag = gi * 16 + a;
+        if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
+        float s = 0.f;
+        for (int q = 0; q < ks; q++) s += partt_at(part, tl2 * ks + q, a, nn);
+        gmem(out)[(int64_t)ag * T.n + row] = s;
+    }
+}
+
+// rq_mmqglu_*_16x<g>: group gi's gate sums (waves 0 .. ks tr - 1) and up sums
+// (the next ks tr) of the workgroup's 32 rows become h = act(g) * u (hf, when
+// set) and, per column, its Q8_1 block (q8_emit4, as rq_quantize_q8_1).
+__device__ __forceinline__ void mmqt_reduce_glu(const RqMmqParams& P, const RqMmqTarget& T, int gi, const float* part) {
+    const int threads = blockDim.x, tid = threadIdx.x, blk = blockIdx.x, ks = P.ks, kt = ks * P.tr;
+    float* hl = (float*)(mmq_lds + P.h_off);  // [16][32]
+    for (int it = tid; it < P.tr * 256; it += threads) {
+        const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15, ag = gi * 16 + a;
+        float gs = 0.f, us = 0.f;
+        for (int q = 0; q < ks; q++) {
+            gs += partt_at(part, tl2 * ks + q, a, nn);
+            us += partt_at(part, kt + tl2 * ks + q, a, nn);
+        }
+        const float h = act_apply(P.act, gs) * us;
+        const int row = (blk * P.tr + tl2) * 16 + nn;
+        if (P.hf && ag < P.m) gmem(P.hf)[(int64_t)ag * T.n + row] = h;
+        hl[a * 32 + tl2 * 16 + nn] = h;
+    }
+    if (!P.hq) return;  // uniform
+    __syncthreads();
+    for (int base = 0; base < 16 * 8; base += threads) {  // uniform trip count: whole 8-lane groups
+        const int t = base + tid;
+        const bool in = t < 16 * 8;
+        const int a = in ? t >> 3 : 0, f4 = t & 7, ag = gi * 16 + a;
+        float h[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) h[j] = hl[a * 32 + 4 * f4 + j];
+        q8_emit4(h, ((int64_t)ag * T.n + blk * 32) / 4 + f4, in && ag < P.m, P.hq, P.hd, P.hs);
+    }
+}
+
 template <int FMT, int SBW, int G, bool GLU>
 __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
     constexpr bool NIB = MF<FMT>::NIB;
@@ -908,44 +954,10 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
     // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
     *(v4f*)(part + (wave * 64 + lane) * 4) = y;
     __syncthreads();
-    if (!GLU) {
-        float* out = (float*)T.out;
-        for (int it = tid; it < P.tr * 256; it += threads) {
-            const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15;
-            const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn, ag = gi * 16 + a;
-            if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
-            float s = 0.f;
-            for (int q = 0; q < ks; q++) s += partt_at(part, tl2 * ks + q, a, nn);
-            gmem(out)[(int64_t)ag * T.n + row] = s;
-        }
-    } else {
-        const int kt = ks * P.tr;
-        float* hl = (float*)(mmq_lds + P.h_off);  // [16][32]
-        for (int it = tid; it < P.tr * 256; it += threads) {
-            const int tl2 = it >> 8, a = (it >> 4) & 15, nn = it & 15, ag = gi * 16 + a;
-            float gs = 0.f, us = 0.f;
-            for (int q = 0; q < ks; q++) {
-                gs += partt_at(part, tl2 * ks + q, a, nn);
-                us += partt_at(part, kt + tl2 * ks + q, a, nn);
-            }
-            const float h = act_apply(P.act, gs) * us;
-            const int row = (blk * P.tr + tl2) * 16 + nn;
-            if (P.hf && ag < P.m) gmem(P.hf)[(int64_t)ag * T.n + row] = h;
-            hl[a * 32 + tl2 * 16 + nn] = h;
-        }
-        if (P.hq) {  // uniform
-            __syncthreads();
-            for (int base = 0; base < 16 * 8; base += threads) {  // uniform trip count: whole 8-lane groups
-                const int t = base + tid;
-                const bool in = t < 16 * 8;
-                const int a = in ? t >> 3 : 0, f4 = t & 7, ag = gi * 16 + a;
-                float h[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) h[j] = hl[a * 32 + 4 * f4 + j];
-                q8_emit4(h, ((int64_t)ag * T.n + blk * 32) / 4 + f4, in && ag < P.m, P.hq, P.hd, P.hs);
-            }
-        }
-    }
+    if (!GLU)
+        mmqt_reduce(P, T, gi, part);
+    else
+        mmqt_reduce_glu(P, T, gi, part);
     }  // column groups
 }
 
@@ -1184,6 +1196,127 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
         mmq_reduce<MP, G, NACC>(P, T);
 }
 
+// 16-column groups over Q6_K (rq_mmq_q6_k_16x<g>_4): mmqt_body's scheme with
+// one MFMA per 16-element sub-block. In the MFMA of window w and k-group c
+// only the A lanes of k-group c hold codes (each lane keeps four A register
+// sets, zero except the one of its own k-group, refreshed by an exec-masked
+// LDS read), so a D entry is the exact dot of sub-block 4w + c of the lane's
+// row with one activation, times 4 (B is 4 (q - 32), rq_params.h). The two
+// sub-blocks of a 32-element block combine in int32 with their signed scales
+// (|sc D| < 2^25), then take the f16 activation scale; per super-block the
+// row's d and the 1/4 apply once. No code-free terms: the -32 is in the codes.
+template <int SBW, int G, bool GLU>
+__device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
+    constexpr int FMT = RQ_FMT_Q6_K;
+    constexpr int NLD = 3 * SBW;  // code loads per lane
+
+    const int tid = threadIdx.x, threads = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, n = lane & 15;
+
+    const int blk = blockIdx.x;
+    int ti = 0, wtl = wave;  // wtl: the wave within its target's waves
+    if (GLU) {  // gate's waves, then up's, on the same tiles
+        ti = wave >= P.ks * P.tr ? 1 : 0;
+        wtl = wave - ti * P.ks * P.tr;
+    } else {
+        if (P.count > 1 && blk >= P.t[1].wg_start) ti = 1;
+        if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
+    }
+    const RqMmqTarget T = pick_target(P, ti);
+    const int ks = P.ks;
+    const int tl = wtl / ks, kpart = wtl - (wtl / ks) * ks;
+    const int tile = (blk - T.wg_start) * P.tr + tl;
+    const bool has_tile = tile < T.tiles;  // wave-uniform
+    const int tile_c = has_tile ? tile : T.tiles - 1;
+    const int S2 = P.S2;
+    const int sb0 = kpart * SBW;
+    const int nsb = min(SBW, S2 - sb0);
+
+    XB x0, x1;
+    mmqt_prefetch(P, 0, x0, x1);
+    // Weights: the row's d of the part's super-blocks (one load; d rows are
+    // padded to a multiple of 8 super-blocks), then per super-block its 16
+    // sub-block scales and its three code loads, the first super-block's now
+    // and each later one's while group 0 computes the one before it.
+    u32 dw[SBW / 2];
+    int4 wv[NLD];
+    int4 hv[SBW];
+    const int DS = (S2 + 7) & ~7;
+    const u8* dp = T.hdr + (int64_t)T.tiles * S2 * 256 + ((int64_t)(tile_c * 16 + n) * DS + sb0) * 2;
+    if (SBW == 2) {
+        dw[0] = ld4_nt(dp);
+    } else {
+        const uint2 v = ld8_nt(dp);
+        dw[0] = v.x;
+        dw[SBW / 2 - 1] = v.y;
+    }
+    const u8* cb = T.code + ((int64_t)tile_c * 3 * S2 + (int64_t)sb0 * 3) * 1024 + lane * 16;
+    const u8* hb = T.hdr + ((int64_t)tile_c * S2 + sb0) * 256 + n * 16;
+    auto load_sb = [&](int i) {
+        hv[i] = ld16_nt(hb + min(i, nsb - 1) * 256);
+#pragma unroll
+        for (int j = 0; j < 3; j++) wv[3 * i + j] = ld16_nt(cb + (int64_t)min(3 * i + j, nsb * 3 - 1) * 1024);
+    };
+    load_sb(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const char* dxp = mmq_lds + P.pl_off;  // f16 dx, [block pair][16][2]
+    float* part = (float*)(mmq_lds + P.part_off);
+    const int ia = lane & 15;
+
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+    mmqt_stage<FMT>(P, gi, x0, x1);
+    if (gi + 1 < G) mmqt_prefetch(P, gi + 1, x0, x1);
+    v4f y = {0.f, 0.f, 0.f, 0.f};
+
+    if (has_tile) {
+        const int xoff = ia * P.kxp + sb0 * 256 + 16 * g;
+        v4i A[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) A[c] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < SBW; i++) {
+            if (i >= nsb) break;  // a short last k-part (uniform)
+            if (gi == 0 && i + 1 < SBW) {
+                load_sb(i + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const int b0 = (sb0 + i) * 8;
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const v4i B = q6_window(wv[3 * i], wv[3 * i + 1], wv[3 * i + 2], w);
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (g == c) A[c] = lds16(xoff + 256 * i + 64 * w);
+                const int4 dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
+                const u32 dxv[4] = {(u32)dxw.x, (u32)dxw.y, (u32)dxw.z, (u32)dxw.w};
+                const u32 sc = (u32)(w == 0 ? hv[i].x : w == 1 ? hv[i].y : w == 2 ? hv[i].z : hv[i].w);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2 * h], B, (v4i{0, 0, 0, 0}), 0, 0, 0);
+                    const v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2 * h + 1], B, (v4i{0, 0, 0, 0}), 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        acc[e] = fmaf((float)q6_pair(sc, 2 * h, 2 * h + 1, Da[e], Db[e]), hsel(dxv[e], h), acc[e]);
+                }
+            }
+            y += (0.25f * half_f(dw[i >> 1], i & 1)) * acc;
+        }
+    }
+    // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
+    *(v4f*)(part + (wave * 64 + lane) * 4) = y;
+    __syncthreads();
+    if (!GLU)
+        mmqt_reduce(P, T, gi, part);
+    else
+        mmqt_reduce_glu(P, T, gi, part);
+    }  // column groups
+}
+
 // Kernel bodies by format. RQ_FMT_MIX_K: launches whose targets mix Q4_K
 // and Q6_K weights of one width (q, k and v of a Q4_K_M layer); a workgroup
 // serves one target, so it branches once, on that target's format, into its
@@ -1286,6 +1419,16 @@ RQ_MMQ_GLU_SET(q6_k, RQ_FMT_Q6_K)
 RQ_MMQT_FMT(q4_0, RQ_FMT_Q4_0)
 RQ_MMQT_FMT(q8_0, RQ_FMT_Q8_0)
 RQ_MMQT_FMT(q4_k, RQ_FMT_Q4_K)
+// Q6_K: one group of 16 (a second group would need its 66 registers of
+// weights held across groups, and spills), 4 super-blocks per wave.
+#define RQ_MMQT6(G)                                                                                        \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_q6_k_16x##G##_4(RqMmqParams p) {              \
+        mmqt6_body<4, G, false>(p);                                                                         \
+    }                                                                                                       \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_q6_k_16x##G(RqMmqParams p) {               \
+        mmqt6_body<4, G, true>(p);                                                                          \
+    }
+RQ_MMQT6(1)
 
 // Mixed Q4_K / Q6_K launches (no block-dot variants: those run per weight).
 #define RQ_MMQ_MIX(MP, SBW)                                                                          \
