@@ -167,10 +167,12 @@ rq_status rq_matvec(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* 
 /* Up to 3 weights of one width sharing xq, one launch (MvTargets,
  * kernels.cu:562-577, backend.rs:1620-1672): of one type, or Q4_K and Q6_K
  * mixed (q/k/v of a Q4_K_M file), and run by one kernel family at this m
- * (a dot4 weight with an MFMA one fails with RQ_ERR_SHAPE). A Q4_K / Q6_K
- * mix on MFMA weights over more than 8 columns runs as one launch per type
- * (the 16-column kernels have no mixed form), so each output is
- * bit-identical to the weight's own rq_matvec. out_lens[i] >= m * rows_i. */
+ * (a dot4 weight with an MFMA one fails with RQ_ERR_SHAPE). Each output is
+ * bit-identical to the weight's own rq_matvec, except a Q4_K weight of a
+ * Q4_K / Q6_K mix on MFMA weights over more than 8 columns: the mixed launch
+ * runs the 8-column kernels, the weight's own launch the 16-column ones
+ * (another summation order, both within the integer path's bound).
+ * out_lens[i] >= m * rows_i. */
 rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, const rq_weight* const* ws, float* const* outs,
                          const int64_t* out_lens, int count);
 

@@ -467,9 +467,6 @@ bool launch_compatible(const rq_weight* a, const rq_weight* b, int64_t m) {
     const bool ma = use_mmq(a, m);
     if (ma != use_mmq(b, m)) return false;
     if (a->type == b->type) return true;
-    // More than 8 MFMA columns run each type in its 16-column classes, which
-    // have no mixed form: a mixed launch would sum in another order.
-    if (ma && m > 8) return false;
     const bool ka = a->fmt == RQ_FMT_Q4_K || a->fmt == RQ_FMT_Q6_K, kb = b->fmt == RQ_FMT_Q4_K || b->fmt == RQ_FMT_Q6_K;
     return ka && kb;
 }
@@ -685,6 +682,22 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
     if (mp == 16) sbw = mmqt_sbw(fmt, S2);
     L.sbw = sbw;
     L.ks = (S2 + sbw - 1) / sbw;
+    if (mp == 16 && ctx->mmq_tr == 0) {
+        // A 16-column workgroup stages 16 columns of the whole row (about 80
+        // to 100 KB at k = 4096), so one fits a CU: the fewest tiles per
+        // workgroup that still run every workgroup in one round. (Q4_K
+        // q and k, 5120 x 4096 at 32 columns: one tile per workgroup took
+        // two rounds, 24.6 us.)
+        const int tr_max = std::max(1, 16 / L.ks);
+        L.tr = 1;
+        for (;;) {
+            mmq_layout(fmt, S2, dots, L);
+            const int64_t per_cu = std::max(1, ctx->lds_wide / std::max(1, L.lds));
+            if ((tiles + L.tr - 1) / L.tr <= ctx->cus * per_cu || L.tr * 2 > tr_max) break;
+            L.tr *= 2;
+        }
+        return L;
+    }
     if (ctx->mmq_tr > 0 || (mp >= 8 && !dots)) {
         const int tr_max = std::max(1, 16 / L.ks);
         if (ctx->mmq_tr > 0) {
@@ -848,6 +861,16 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
         L.ks = (S2 + 3) / 4;
         L.tr = 2;
         mmq_layout(fmt, S2, false, L);
+        // A 16-column workgroup (one per CU for its LDS) only where all of
+        // them run in one round (Llama-3-8B's 14336-row FFN at 32 columns:
+        // 448 workgroups, 40.2 us, against 8-column ones three to a CU).
+        if (L.mp == 16 && gate->tiles / 2 > (int64_t)ctx->cus * std::max(1, ctx->lds_wide / (L.lds + 2 * L.ks * L.tr * 1024 + 2048))) {
+            L = mmq_cols(fmt, S2, nc, false);
+            L.sbw = 4;
+            L.ks = (S2 + 3) / 4;
+            L.tr = 2;
+            mmq_layout(fmt, S2, false, L);
+        }
         if (L.mp == 16) {  // both weights' partials of one group; h of one group
             h_off = L.part_off + 2 * L.ks * L.tr * 64 * 4 * 4;
             L.lds = h_off + 16 * 32 * 4;
@@ -1538,9 +1561,7 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matvec: output %d not 4-byte aligned", i);
         if (use_mmq(ws[i], m) != use_mmq(ws[0], m))
             return fail(RQ_ERR_SHAPE, "matvec: weights laid out for different kernel families in one launch");
-        const bool kq = (ws[0]->fmt == RQ_FMT_Q4_K || ws[0]->fmt == RQ_FMT_Q6_K) &&
-                        (ws[i]->fmt == RQ_FMT_Q4_K || ws[i]->fmt == RQ_FMT_Q6_K);
-        if (ws[i]->type != ws[0]->type && !kq)
+        if (!launch_compatible(ws[0], ws[i], m))
             return fail(RQ_ERR_SHAPE, "matvec: mixed weight types %s and %s in one launch", type_name(ws[0]->type),
                         type_name(ws[i]->type));
         if (ws[i]->cols != ws[0]->cols)
@@ -1554,23 +1575,7 @@ extern "C" rq_status rq_matvec_many(rq_ctx* ctx, const rq_q8_1* xq, int64_t m, c
         if ((st = check_len("matmul out", out_lens[i], m * ws[i]->rows)) != RQ_OK) return st;
     if (m == 0) return RQ_OK;
     if ((st = bind(ctx)) != RQ_OK) return st;
-    if (use_mmq(ws[0], m)) {
-        bool one = true;  // Q4_K with Q6_K past 8 columns: a launch per type (launch_compatible)
-        for (int i = 1; i < count; i++) one = one && launch_compatible(ws[0], ws[i], m);
-        if (one) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
-        for (int f : {RQ_FMT_Q4_K, RQ_FMT_Q6_K}) {
-            const rq_weight* sw[RQ_MV_TARGETS];
-            void* so[RQ_MV_TARGETS];
-            int c = 0;
-            for (int i = 0; i < count; i++)
-                if (ws[i]->fmt == f) {
-                    sw[c] = ws[i];
-                    so[c++] = outs[i];
-                }
-            if (c && (st = mmq_launch(ctx, xq->qs, xq->d, nullptr, m, sw, so, c, false)) != RQ_OK) return st;
-        }
-        return RQ_OK;
-    }
+    if (use_mmq(ws[0], m)) return mmq_launch(ctx, xq->qs, xq->d, nullptr, m, ws, (void* const*)outs, count, false);
     return matvec_launch(ctx, xq->qs, xq->d, nullptr, m, ws, outs, count);
 }
 

@@ -350,7 +350,9 @@ def test_mixed_q4k_q6k_launch(gpu, orc, family, k, m):
     """q, k (Q4_K) and v (Q6_K) of a Q4_K_M layer share one launch (dot4:
     rq_mvxm / rq_mvfm; MFMA: rq_mmq_q4_k_q6_k_*, a workgroup running its
     target's format): each output is bit-identical to its own single-weight
-    launch."""
+    launch, except MFMA Q4_K over more than 8 columns, whose own launch runs
+    the 16-column kernels (another summation order; both within 1e-3 of the
+    integer oracle, checked here)."""
     if family == "mfma" and k > 16384:
         pytest.skip("Q6_K over 16384 columns runs the dot4 kernels")
     spec = [(12, 64), (12, 16), (14, 16)] if k <= 4096 else [(12, 12), (14, 5), (12, 7)]
@@ -367,13 +369,20 @@ def test_mixed_q4k_q6k_launch(gpu, orc, family, k, m):
     xq = gpu.quantize_q8_1(x, m, k)
     via_q8 = [gpu.alloc(m * n) for _, n in spec]
     gpu.matvec_many(xq, wgs, via_q8, m)
-    for (t, n), wg, a, b in zip(spec, wgs, together, via_q8):
+    qs, d, _ = orc.quantize_q8_1(_x(orc, 701, m, k), m, k)
+    for (t, n), w, wg, a, b in zip(spec, ws, wgs, together, via_q8):
         alone = gpu.alloc(m * n)
         gpu.matmul(x, wg, alone, m)
-        want = gpu.to_host(alone, m * n).view(np.uint32)
-        assert np.array_equal(gpu.to_host(a, m * n).view(np.uint32), want), f"type {t} rows {n} (matmul_many)"
         alone_q = gpu.alloc(m * n)
         gpu.matvec(xq, wg, alone_q, m)
+        if family == "mfma" and m > 8 and t == 12:
+            want = orc.matvec_q8_1(t, w, n, k, qs, d, m)
+            for got in (a, b, alone, alone_q):
+                orc.assert_close(f"type {t} rows {n} m={m}", want, gpu.to_host(got, m * n), TOL_B)
+            assert np.array_equal(gpu.to_host(a, m * n).view(np.uint32), gpu.to_host(b, m * n).view(np.uint32))
+            continue
+        want = gpu.to_host(alone, m * n).view(np.uint32)
+        assert np.array_equal(gpu.to_host(a, m * n).view(np.uint32), want), f"type {t} rows {n} (matmul_many)"
         assert np.array_equal(gpu.to_host(b, m * n).view(np.uint32),
                               gpu.to_host(alone_q, m * n).view(np.uint32)), f"type {t} rows {n} (matvec_many)"
 
