@@ -112,8 +112,8 @@ rq_status rq_set_stream(rq_ctx* ctx, void* stream);
  *                    batching);
  *   RQ_KERNELS_BOTH  both layouts (twice the device memory): each call runs
  *                    dot4 below 4 activation columns and MFMA from 4 up.
- * Widths the MFMA kernels cannot stage (Q4_0 / Q4_K: cols > 32768, Q8_0 /
- * Q6_K: cols > 16384) fall back to dot4. Both families compute the same int32 block
+ * Widths the MFMA kernels cannot stage (cols > 65536) fall back to dot4.
+ * Both families compute the same int32 block
  * dots; their f32 sums differ only in accumulation order. The environment
  * variable RQ_KERNELS=auto|dot4|mfma|both sets the default at rq_open. */
 #define RQ_KERNELS_AUTO 0

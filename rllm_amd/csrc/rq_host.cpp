@@ -250,6 +250,10 @@ struct rq_ctx {
     // fused gate/up + activation (sbw 4): column classes 1, 4, 8, 8x2, 8x4; f32 x
     hipFunction_t mmqglu[RQ_NUM_FMTS][5] = {};
     hipFunction_t mmqgluf[RQ_NUM_FMTS] = {};
+    // Wide rows (passes): [mp index] (1, 4, 8), then the f32 one at [3].
+    hipFunction_t mmqw[RQ_NUM_FMTS + 1][4] = {};
+    hipFunction_t mmqdw[RQ_NUM_FMTS][3] = {};
+    hipFunction_t mmqgluw[RQ_NUM_FMTS][4] = {};
     hipFunction_t mmq_repack[RQ_NUM_FMTS] = {};
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
@@ -586,10 +590,20 @@ int mmq_S2(int64_t cols) { return (int)((cols + 511) / 512 * 2); }
 // f16 row scales d per Q6_K row (super-blocks, padded to a multiple of 8).
 int64_t mmq_d_stride(int S2) { return (S2 + 7) / 8 * 8; }
 
-// A workgroup holds the ks <= 16 waves of a tile's k-parts.
+// A workgroup holds the ks <= 16 waves of a tile's k-parts. Rows of more
+// than 64 super-blocks (k > 16384) run the wide kernels (rq_mmq*_w*:
+// single-group classes, up to 8 columns per launch, 16 k-parts of 4
+// super-blocks per tile), whose waves walk the row in np passes, the same
+// for every format, so that Q4_K in a launch mixed with Q6_K sums as in its
+// own. Rows up to 65536 wide, whose one-column staging (64 KB of codes)
+// fits a workgroup's LDS.
 bool mmq_supported(int fmt, int64_t cols) {
-    const int maxs = mmq_sbw_max(fmt);
-    return (mmq_S2(cols) + maxs - 1) / maxs <= 16;
+    (void)fmt;
+    return mmq_S2(cols) <= 256;
+}
+int mmq_np(int fmt, int S2) {
+    (void)fmt;
+    return S2 > 64 ? ((S2 + 3) / 4 + 15) / 16 : 1;
 }
 
 // Columns per launch: up to 8 in one staged group (mp = 1, 4, 8), or 8 x g
@@ -604,7 +618,9 @@ bool mmq_has_t(int fmt, int S2) { return fmt != RQ_FMT_MIX_K && (S2 + 3) / 4 <= 
 // Q6_K runs the 16-column kernels for up to 16 columns only: holding its
 // weights for a second group makes them spill.
 int mmqt_max_cols(int fmt) { return fmt == RQ_FMT_Q6_K ? 16 : 64; }
-int mmq_max_cols(int fmt, int S2) { return mmq_has_t(fmt, S2) && fmt != RQ_FMT_Q6_K ? 64 : 32; }
+int mmq_max_cols(int fmt, int S2) {
+    return mmq_np(fmt, S2) > 1 ? 8 : mmq_has_t(fmt, S2) && fmt != RQ_FMT_Q6_K ? 64 : 32;
+}
 // Group-count index of a 16-column class (g = 1, 2, 4).
 int mmqt_g_index(int g) { return g == 1 ? 0 : g == 2 ? 1 : 2; }
 // Super-blocks per wave of a 16-column launch: 4 for Q4_K; 2 for Q4_0 and
@@ -616,12 +632,19 @@ int mmqt_sbw(int fmt, int S2) { return fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q6_K 
 struct MmqPlan {
     int mp, g, sbw, ks, tr;  // mp = 16: the 16-column classes
     int kxp, pl_off, part_off, lds;
+    int np;  // passes per wave over the row (1 unless ks would exceed 16)
 };
 
 // Kernel table index of a format (RQ_FMT_MIX_K: the mixed Q4_K / Q6_K kernels).
 int mmq_fi(int fmt) { return fmt == RQ_FMT_MIX_K ? RQ_NUM_FMTS : fmt; }
 
 hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, const MmqPlan& L, bool f32_in, bool dots) {
+    if (L.np > 1) {
+        if (L.mp > 8 || L.g > 1 || L.sbw != 4) return nullptr;
+        const int mi = mmq_mp_index(L.mp);
+        if (dots) return fmt == RQ_FMT_MIX_K ? nullptr : ctx->mmqdw[fmt][mi];
+        return ctx->mmqw[mmq_fi(fmt)][f32_in ? 3 : mi];
+    }
     if (L.mp == 16) {
         if (L.sbw != 2 && L.sbw != 4) return nullptr;
         return ctx->mmqt[fmt][mmqt_g_index(L.g)][L.sbw == 2 ? 0 : 1];
@@ -680,8 +703,10 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
     else if (mp >= 8 && !dots)
         sbw = std::max(sbw, std::min(4, maxs));
     if (mp == 16) sbw = mmqt_sbw(fmt, S2);
+    L.np = mmq_np(fmt, S2);
+    if (L.np > 1) sbw = 4;  // the wide kernels: 16 k-parts of 4 per tile, in passes
     L.sbw = sbw;
-    L.ks = (S2 + sbw - 1) / sbw;
+    L.ks = L.np > 1 ? 16 : (S2 + sbw - 1) / sbw;
     if (mp == 16 && ctx->mmq_tr == 0) {
         // A 16-column workgroup stages 16 columns of the whole row (about 80
         // to 100 KB at k = 4096), so one fits a CU: the fewest tiles per
@@ -824,6 +849,7 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
         p.kxp = P.kxp;
         p.pl_off = P.pl_off;
         p.part_off = P.part_off;
+        p.np = P.np;
         hipFunction_t f = mmq_kernel(ctx, fmt, P, xf != nullptr, dots);
         if (!f) return fail(RQ_ERR_UNSUPPORTED, "matvec: no MFMA kernel for %d x %d columns, %d super-blocks per wave",
                             P.mp, P.g, P.sbw);
@@ -836,12 +862,15 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
 }
 
 // Fused gate/up + activation over the MFMA layout (rq_mmqglu_*): gate and up
-// of one type and shape whose two weights' k-parts (4 super-blocks per wave)
-// of two 16-row tiles fit one workgroup (rows of at most 16 super-blocks),
-// n % 32 == 0 (a workgroup's 32 rows are one Q8_1 block of h per column).
+// of one type and shape, n % 32 == 0 (a workgroup's 32 rows are one Q8_1
+// block of h per column). A workgroup holds the two weights' k-parts (4
+// super-blocks per wave) of two 16-row tiles: rows of up to 16 super-blocks
+// in one pass; wider rows (up to kGluMaxS2, k <= 32768) in passes of 4 waves
+// per tile and weight, at most 8 columns per launch.
+constexpr int kGluMaxS2 = 128;
 bool glu_mmq_ok(const rq_weight* gate, const rq_weight* up, int64_t m) {
     return use_mmq(gate, m) && use_mmq(up, m) && gate->type == up->type && gate->rows == up->rows &&
-           gate->cols == up->cols && gate->rows % 32 == 0 && gate->S2 <= 16;
+           gate->cols == up->cols && gate->rows % 32 == 0 && gate->S2 <= kGluMaxS2;
 }
 
 // h = act(x . gate) * (x . up) into hf (may be null) and the Q8_1 (hq, hd,
@@ -852,13 +881,17 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
                          uint16_t* hs) {
     const int fmt = gate->fmt, S2 = gate->S2;
     const int64_t k = gate->cols, n = gate->rows, U = k / 32;
+    // Rows of more than 16 super-blocks: 4 k-parts per tile and weight, each
+    // wave walking `np` passes of the row (single-group classes only).
+    const bool wide = S2 > 16;
+    const int np = wide ? ((S2 + 3) / 4 + 3) / 4 : 1;
     auto plan = [&](int nc, MmqPlan& L, int& h_off) {
         // The 16-column classes at 4 super-blocks per wave hold their weights
         // across groups without spilling only for Q4_K up to two groups and
         // for every type at one.
-        L = mmq_cols(fmt, S2, nc, nc <= (fmt == RQ_FMT_Q4_K ? 32 : 16));
+        L = mmq_cols(fmt, S2, nc, !wide && nc <= (fmt == RQ_FMT_Q4_K ? 32 : 16));
         L.sbw = 4;
-        L.ks = (S2 + 3) / 4;
+        L.ks = wide ? 4 : (S2 + 3) / 4;
         L.tr = 2;
         mmq_layout(fmt, S2, false, L);
         // A 16-column workgroup (one per CU for its LDS) only where all of
@@ -879,7 +912,7 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
             L.lds = h_off + L.g * L.mp * 32 * 4;
         }
     };
-    const int max_cols = xf ? 1 : 32;  // the classes above take at most 32
+    const int max_cols = xf ? 1 : wide ? 8 : 32;  // the classes above take at most 32
     int64_t ngroups = (m + max_cols - 1) / max_cols;
     for (;;) {
         MmqPlan L;
@@ -925,10 +958,12 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
         p.hd = hq ? hd + g0 * n / 32 : nullptr;
         p.hs = hq ? hs + g0 * n / 32 : nullptr;
         p.act = act;
+        p.np = np;
         const int cls = L.g > 1 ? (L.g == 2 ? 3 : 4) : mmq_mp_index(L.mp);
-        hipFunction_t f = xf     ? ctx->mmqgluf[fmt]
+        hipFunction_t f = wide       ? ctx->mmqgluw[fmt][xf ? 3 : mmq_mp_index(L.mp)]
+                          : xf         ? ctx->mmqgluf[fmt]
                           : L.mp == 16 ? ctx->mmqglut[fmt][mmqt_g_index(L.g)]
-                                 : ctx->mmqglu[fmt][cls];
+                                       : ctx->mmqglu[fmt][cls];
         rq_status st = launch(ctx, f, xf ? "rq_mmqgluf" : "rq_mmqglu", (uint64_t)(gate->tiles / 2), &p,
                               (unsigned)L.lds, (unsigned)(64 * 2 * L.ks * L.tr));
         if (st != RQ_OK) return st;
@@ -1145,6 +1180,21 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
         }
         snprintf(name, sizeof name, "rq_mmqgluf_%s", kFmtSuffix[f]);
         if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmqgluf[f], name);
+    }
+    for (int f = 0; f <= RQ_NUM_FMTS && st == RQ_OK; f++) {  // wide rows
+        const char* fs = f == RQ_NUM_FMTS ? "q4_k_q6_k" : kFmtSuffix[f];
+        for (int mi = 0; mi < 3 && st == RQ_OK; mi++) {
+            snprintf(name, sizeof name, "rq_mmq_%s_w%d", fs, kMmqMp[mi]);
+            if ((st = getm(ctx->mmq_mod, &ctx->mmqw[f][mi], name)) != RQ_OK || f == RQ_NUM_FMTS) continue;
+            snprintf(name, sizeof name, "rq_mmqd_%s_w%d", fs, kMmqMp[mi]);
+            if ((st = getm(ctx->mmq_mod, &ctx->mmqdw[f][mi], name)) != RQ_OK) break;
+            snprintf(name, sizeof name, "rq_mmqglu_%s_w%d", fs, kMmqMp[mi]);
+            st = getm(ctx->mmq_mod, &ctx->mmqgluw[f][mi], name);
+        }
+        snprintf(name, sizeof name, "rq_mmqf_%s_w", fs);
+        if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmqw[f][3], name);
+        snprintf(name, sizeof name, "rq_mmqgluf_%s_w", fs);
+        if (st == RQ_OK && f < RQ_NUM_FMTS) st = getm(ctx->mmq_mod, &ctx->mmqgluw[f][3], name);
     }
     for (int si = 0; si < 2 && st == RQ_OK; si++) {  // mixed Q4_K / Q6_K: sbw 2 and 4
         const int fi = RQ_NUM_FMTS;

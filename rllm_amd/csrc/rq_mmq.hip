@@ -413,7 +413,7 @@ __device__ __forceinline__ void mmq_reduce_glu(const RqMmqParams& P, const RqMmq
 // G > 1 (mp = 8): the launch's columns come in G groups of 8 that are staged
 // and computed one after another through the same LDS, against weights loaded
 // once into registers.
-template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
+template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false, bool WIDE = false>
 __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr bool NIB = MF<FMT>::NIB;
     constexpr int PS = 16 / MP;                // D rows (slots) per activation
@@ -447,8 +447,14 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
     const int S2 = P.S2;
-    const int sb0 = kpart * SBW;           // first super-block of the part
-    const int nsb = min(SBW, S2 - sb0);    // even, >= 2
+    // Pass p of the wave takes super-blocks (p ks + kpart) sbw .. (+ sbw).
+    // One pass, except in the wide kernels (rq_mmq*_w*: rows of more than
+    // ks k-parts, the fused FFN past 16 super-blocks and matvecs past 16
+    // k-parts), whose waves walk the row, each pass's loads issued after the
+    // pass before.
+    const int np = WIDE ? max(1, P.np) : 1;
+    int sb0 = kpart * SBW;         // first super-block of the pass
+    int nsb = min(SBW, S2 - sb0);  // even, >= 2 in pass 0
 
     // ---- Round 0 of the staging loads, then every weight load of the wave.
     XB x0;
@@ -465,7 +471,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr int LPH = NLD / NH;  // code loads per header
     int4 wv[NLD];
     int4 hv[NH];
-    {
+    auto load_w = [&]() {
         const int nvalid = nsb * LPS;
         const u8* cb = T.code + ((int64_t)tile_c * LPS * S2 + (int64_t)sb0 * LPS) * 1024 + lane * 16;
         const u8* hb = T.hdr + ((int64_t)tile_c * S2 + sb0) * 256 + n * 16;
@@ -477,7 +483,8 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
             for (int j = 0; j < LPH; j++)
                 wv[i * LPH + j] = ld16_nt(cb + (int64_t)min(i * LPH + j, nvalid - 1) * 1024);
         }
-    }
+    };
+    load_w();
     __builtin_amdgcn_sched_barrier(0);
 
     // Q4_K: the lane's decoded headers (q4k_decode), filled by column group 0
@@ -493,6 +500,13 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
     for (int e = 0; e < NACC; e++) y[e] = 0.f;
 
+    for (int pass = 0; pass < np; pass++) {
+    if (pass > 0) {
+        sb0 = (pass * ks + kpart) * SBW;
+        nsb = min(SBW, S2 - sb0);
+        if (nsb <= 0 || !has_tile) break;  // wave-uniform
+        load_w();
+    }
     if (has_tile) {
         // A operand: row ia = lane % 16 of A is (activation ia / PS, slot ia % PS);
         // it is live in phase (slot / 2) for k-groups of half (slot % 2).
@@ -665,6 +679,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
             }
         }
     }
+    }  // passes
     if (!DOTS) mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
     }  // column groups
     if (DOTS) return;
@@ -999,7 +1014,7 @@ __device__ __forceinline__ int q6_pair(u32 sc, int a, int b, int Da, int Db) {
     return __mul24(sbyte(sc, a), Da) + __mul24(sbyte(sc, b), Db);
 }
 
-template <int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
+template <int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false, bool WIDE = false>
 __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     constexpr int FMT = RQ_FMT_Q6_K;
     constexpr int NLD = 3 * SBW;               // code loads per lane
@@ -1027,8 +1042,10 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     const bool has_tile = tile < T.tiles;  // wave-uniform
     const int tile_c = has_tile ? tile : T.tiles - 1;
     const int S2 = P.S2;
-    const int sb0 = kpart * SBW;
-    const int nsb = min(SBW, S2 - sb0);
+    // Passes over rows wider than the ks k-parts, as in mmq_body.
+    const int np = WIDE ? max(1, P.np) : 1;
+    int sb0 = kpart * SBW;
+    int nsb = min(SBW, S2 - sb0);
 
     // ---- Round 0 of the staging loads, then the weight loads: the row's d
     // of the part's super-blocks (one load; the d rows are padded to a
@@ -1045,7 +1062,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     int4 wv[NLD];
     int4 hv[MP == 1 ? 1 : SBW];
     u32 h1[MP == 1 ? SBW : 1];
-    {
+    auto load_w = [&]() {
         const int DS = (S2 + 7) & ~7;
         const u8* dp = T.hdr + (int64_t)T.tiles * S2 * 256 + ((int64_t)(tile_c * 16 + n) * DS + sb0) * 2;
         if (SBW == 2) {
@@ -1068,7 +1085,8 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
             for (int j = 0; j < 3; j++) wv[3 * i + j] = ld16_nt(cb + (int64_t)min(3 * i + j, nvalid - 1) * 1024);
         }
-    }
+    };
+    load_w();
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -1078,6 +1096,13 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
     for (int e = 0; e < NACC; e++) y[e] = 0.f;
 
+    for (int pass = 0; pass < np; pass++) {
+    if (pass > 0) {
+        sb0 = (pass * ks + kpart) * SBW;
+        nsb = min(SBW, S2 - sb0);
+        if (nsb <= 0 || !has_tile) break;  // wave-uniform
+        load_w();
+    }
     if (has_tile) {
         // A row ia = lane % 16 and the phase the lane is live in (-1: none):
         //   mp = 1  row (window ia / 4, k-group ia % 4), phase = window
@@ -1183,6 +1208,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
             for (int e = 0; e < NACC; e++) y[e] = fmaf(dsb, acc[e], y[e]);
         }
     }
+    }  // passes
     if (!DOTS) {
 #pragma unroll
         for (int e = 0; e < NACC; e++) y[e] *= 0.25f;
@@ -1321,10 +1347,10 @@ __device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
 // and Q6_K weights of one width (q, k and v of a Q4_K_M layer); a workgroup
 // serves one target, so it branches once, on that target's format, into its
 // body (staging included; the host sizes LDS for Q4_K's two planes).
-template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false>
+template <int FMT, int MP, int SBW, bool F32IN, bool DOTS, int G = 1, bool GLU = false, bool WIDE = false>
 __device__ __forceinline__ void mmq_run(const RqMmqParams& P) {
     if constexpr (FMT == RQ_FMT_Q6_K) {
-        mmq6_body<MP, SBW, F32IN, DOTS, G, GLU>(P);
+        mmq6_body<MP, SBW, F32IN, DOTS, G, GLU, WIDE>(P);
     } else if constexpr (FMT == RQ_FMT_MIX_K) {
         const int blk = blockIdx.x;
         int ti = 0;
@@ -1332,11 +1358,11 @@ __device__ __forceinline__ void mmq_run(const RqMmqParams& P) {
         if (P.count > 2 && blk >= P.t[2].wg_start) ti = 2;
         const int fmt = pick_target(P, ti).fmt;  // workgroup-uniform
         if (fmt == RQ_FMT_Q6_K)
-            mmq6_body<MP, SBW, F32IN, DOTS, G>(P);
+            mmq6_body<MP, SBW, F32IN, DOTS, G, false, WIDE>(P);
         else
-            mmq_body<RQ_FMT_Q4_K, MP, SBW, F32IN, DOTS, G>(P);
+            mmq_body<RQ_FMT_Q4_K, MP, SBW, F32IN, DOTS, G, false, WIDE>(P);
     } else {
-        mmq_body<FMT, MP, SBW, F32IN, DOTS, G, GLU>(P);
+        mmq_body<FMT, MP, SBW, F32IN, DOTS, G, GLU, WIDE>(P);
     }
 }
 
@@ -1399,6 +1425,59 @@ RQ_MMQ_GLU_SET(q4_0, RQ_FMT_Q4_0)
 RQ_MMQ_GLU_SET(q8_0, RQ_FMT_Q8_0)
 RQ_MMQ_GLU_SET(q4_k, RQ_FMT_Q4_K)
 RQ_MMQ_GLU_SET(q6_k, RQ_FMT_Q6_K)
+
+// Wide rows (passes): the single-group classes, 4 super-blocks per wave
+// (rq_mmq*_<fmt>_w<mp>; at 8 the Q4 formats' passes spill), and the fused
+// FFN's.
+#define RQ_MMQ_WIDE(NAME, FMT, SBW)                                                                   \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_##NAME##_w1(RqMmqParams p) {            \
+        mmq_run<FMT, 1, SBW, false, false, 1, false, true>(p);                                        \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_##NAME##_w4(RqMmqParams p) {            \
+        mmq_run<FMT, 4, SBW, false, false, 1, false, true>(p);                                        \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmq_##NAME##_w8(RqMmqParams p) {            \
+        mmq_run<FMT, 8, SBW, false, false, 1, false, true>(p);                                        \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqf_##NAME##_w(RqMmqParams p) {            \
+        mmq_run<FMT, 1, SBW, true, false, 1, false, true>(p);                                         \
+    }
+#define RQ_MMQ_WIDE_DOTS(NAME, FMT, SBW)                                                              \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqd_##NAME##_w1(RqMmqParams p) {           \
+        mmq_run<FMT, 1, SBW, false, true, 1, false, true>(p);                                         \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqd_##NAME##_w4(RqMmqParams p) {           \
+        mmq_run<FMT, 4, SBW, false, true, 1, false, true>(p);                                         \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqd_##NAME##_w8(RqMmqParams p) {           \
+        mmq_run<FMT, 8, SBW, false, true, 1, false, true>(p);                                         \
+    }
+#define RQ_MMQ_GLU_WIDE(NAME, FMT)                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_w1(RqMmqParams p) {         \
+        mmq_run<FMT, 1, 4, false, false, 1, true, true>(p);                                           \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_w4(RqMmqParams p) {         \
+        mmq_run<FMT, 4, 4, false, false, 1, true, true>(p);                                           \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_w8(RqMmqParams p) {         \
+        mmq_run<FMT, 8, 4, false, false, 1, true, true>(p);                                           \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void rq_mmqgluf_##NAME##_w(RqMmqParams p) {         \
+        mmq_run<FMT, 1, 4, true, false, 1, true, true>(p);                                            \
+    }
+RQ_MMQ_WIDE(q4_0, RQ_FMT_Q4_0, 4)
+RQ_MMQ_WIDE(q8_0, RQ_FMT_Q8_0, 4)
+RQ_MMQ_WIDE(q4_k, RQ_FMT_Q4_K, 4)
+RQ_MMQ_WIDE(q6_k, RQ_FMT_Q6_K, 4)
+RQ_MMQ_WIDE(q4_k_q6_k, RQ_FMT_MIX_K, 4)
+RQ_MMQ_WIDE_DOTS(q4_0, RQ_FMT_Q4_0, 4)
+RQ_MMQ_WIDE_DOTS(q8_0, RQ_FMT_Q8_0, 4)
+RQ_MMQ_WIDE_DOTS(q4_k, RQ_FMT_Q4_K, 4)
+RQ_MMQ_WIDE_DOTS(q6_k, RQ_FMT_Q6_K, 4)
+RQ_MMQ_GLU_WIDE(q4_0, RQ_FMT_Q4_0)
+RQ_MMQ_GLU_WIDE(q8_0, RQ_FMT_Q8_0)
+RQ_MMQ_GLU_WIDE(q4_k, RQ_FMT_Q4_K)
+RQ_MMQ_GLU_WIDE(q6_k, RQ_FMT_Q6_K)
 
 // 16 x g columns (Q4_0, Q8_0, Q4_K; sbw 2, 4) and the fused gate/up of the
 // same classes (sbw 4).

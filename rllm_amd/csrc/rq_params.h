@@ -205,7 +205,7 @@ struct RqMmqParams {
     uint16_t* hd;
     uint16_t* hs;
     int32_t act;
-    int32_t pad;
+    int32_t np;  // passes per wave over the row (rows wider than ks * sbw super-blocks; 0 or 1: one)
 };
 
 struct RqMmqRepackParams {

@@ -206,6 +206,31 @@ def test_gated_ffn_q8_1_input(gpuk, orc, tname, m):
     assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32)), "out"
 
 
+@pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("d", [5120, 8192, 14336, 20480])
+@pytest.mark.parametrize("m", [1, 3, 8, 12])
+def test_gated_ffn_wide_inputs(gpuk, orc, tname, d, m):
+    """Inputs wider than 16 super-blocks: the fused MFMA front half walks the
+    row in passes (rq_mmqglu_*_w*, up to 8 columns per launch), the dot4 one
+    in its own way. h within 1e-3 of the int8 oracle; the down projection
+    reads exactly the Q8_1 of h."""
+    t, f = TYPES[tname], 256
+    gw = orc.random_weight(0xE0 + m, t, f, d)
+    uw = orc.random_weight(0xE1 + m, t, f, d)
+    dw = orc.random_weight(0xE2 + m, t, d, f)
+    g, u, dn = upload(gpuk, t, gw, f, d), upload(gpuk, t, uw, f, d), upload(gpuk, t, dw, d, f)
+    x = orc.normal(0xE3 + d + m, m * d, 0.0, 1.0)
+    out, gb, ub = gpuk.alloc(m * d), gpuk.alloc(m * f), gpuk.alloc(m * f)
+    gpuk.gated_ffn(gpuk.from_host(x), g, u, dn, Activation.SILU, out, gb, ub, m)
+    h = gpuk.to_host(gb, m * f)
+    qs, dq, _ = orc.quantize_q8_1(x, m, d)
+    want_h = orc.glu_q8_1(t, gw, uw, f, d, qs, dq, m, int(Activation.SILU))
+    orc.assert_close(f"h {tname} d={d} m={m}", want_h, h, 1e-3)
+    want = gpuk.alloc(m * d)
+    gpuk.matvec(gpuk.quantize_q8_1(gb, m, f), dn, want, m)
+    assert np.array_equal(gpuk.to_host(out, m * d).view(np.uint32), gpuk.to_host(want, m * d).view(np.uint32))
+
+
 @pytest.mark.parametrize("tname", ["Q4_K", "Q8_0", "Q4_0", "Q6_K"])
 @pytest.mark.parametrize("m", [1, 4, 8, 16, 33])
 @pytest.mark.parametrize("act", ACTS)

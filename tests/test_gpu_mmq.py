@@ -53,14 +53,13 @@ def test_mmq_column_classes(mfma, orc, tname, m):
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
-@pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480])
+@pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480, 36864])
 @pytest.mark.parametrize("m", [1, 3, 8, 20])
 def test_mmq_widths(mfma, orc, tname, k, m):
-    """Odd super-block counts (zero padding to an even count), 2/4/8 super-blocks per wave."""
-    t = MMQ_TYPES[tname]
-    if t in (8, 14) and k > 16384:
-        pytest.skip(f"{tname} over 16384 columns runs the dot4 kernels")
-    _run(mfma, orc, t, 33, k, m, 17 * k + m, kind="normal")
+    """Odd super-block counts (zero padding to an even count), 2/4 super-blocks
+    per wave; rows of more than 64 super-blocks (past 16384 columns) in the
+    wide kernels' passes (2 and 3 passes here)."""
+    _run(mfma, orc, MMQ_TYPES[tname], 33, k, m, 17 * k + m, kind="normal")
 
 
 @pytest.mark.parametrize("tname", ["Q4_0", "Q8_0"])
@@ -146,9 +145,9 @@ def test_mixed_families_in_one_launch_is_an_error(gpu, orc):
 
 @pytest.mark.parametrize("tname", ["Q8_0", "Q6_K"])
 def test_mmq_wide_rows_fall_back_to_dot4(gpu, orc, tname):
-    """Formats whose MFMA kernels stop at 4 super-blocks per wave take the
-    dot4 layout past 16384 columns, also when MFMA is selected."""
-    t, n, k = MMQ_TYPES[tname], 20, 16384 + 1024
+    """Rows wider than 65536 (one column's staging past 64 KB of LDS) take
+    the dot4 layout, also when MFMA is selected."""
+    t, n, k = MMQ_TYPES[tname], 20, 65536 + 1024
     w = make_weight(orc, t, n, k, 5, "random")
     gpu.set_kernels("mfma")
     try:

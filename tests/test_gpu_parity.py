@@ -353,8 +353,6 @@ def test_mixed_q4k_q6k_launch(gpu, orc, family, k, m):
     launch, except MFMA Q4_K over more than 8 columns, whose own launch runs
     the 16-column kernels (another summation order; both within 1e-3 of the
     integer oracle, checked here)."""
-    if family == "mfma" and k > 16384:
-        pytest.skip("Q6_K over 16384 columns runs the dot4 kernels")
     spec = [(12, 64), (12, 16), (14, 16)] if k <= 4096 else [(12, 12), (14, 5), (12, 7)]
     ws = [make_weight(orc, t, n, k, 700 + i, "random") for i, (t, n) in enumerate(spec)]
     gpu.set_kernels(family)
