@@ -54,11 +54,12 @@ def test_mmq_column_classes(mfma, orc, tname, m):
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
 @pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480, 36864])
-@pytest.mark.parametrize("m", [1, 3, 8, 20])
+@pytest.mark.parametrize("m", [1, 3, 8, 16, 20])
 def test_mmq_widths(mfma, orc, tname, k, m):
     """Odd super-block counts (zero padding to an even count), 2/4 super-blocks
     per wave; rows of more than 64 super-blocks (past 16384 columns) in the
-    wide kernels' passes (2 and 3 passes here)."""
+    wide kernels' passes (2 and 3 passes here); 16 columns in one
+    16-column launch where the staging fits, else in 8-column groups."""
     _run(mfma, orc, MMQ_TYPES[tname], 33, k, m, 17 * k + m, kind="normal")
 
 
