@@ -655,6 +655,12 @@ hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, const MmqPlan& L, bool f32_
     return f32_in ? ctx->mmqf[fi][si] : ctx->mmq[fi][mi][si];
 }
 
+// End of a 16-column layout's activation planes (block-major f16 scales;
+// Q4_K / Q4_0 also f = dx sum q in f32).
+int mmqt_planes_end(int fmt, int S2, const MmqPlan& L) {
+    return L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q4_0 ? 6 : 2);
+}
+
 void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
     if (L.mp == 16) {
         // 16 B of skew: the 16 lanes of one k-group read 16 B of each of the
@@ -663,7 +669,12 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
         // Q8_0); the partial sums of one group.
         L.kxp = S2 * 256 + 16;
         L.pl_off = 16 * L.kxp;
-        L.part_off = L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q4_0 ? 6 : 2);
+        // The partial sums of one group after the planes. (Over the staged
+        // codes, as the fused FFN puts them, a 16-column matvec fits two
+        // workgroups to a CU, and the planner's fewer tiles per workgroup ran
+        // slower: Q4_K 14336 x 4096 at 16 / 32 / 64 columns 11.7 / 19.3 /
+        // 34.4 -> 13.3 / 22.4 / 41.1 us.)
+        L.part_off = mmqt_planes_end(fmt, S2, L);
         L.lds = L.part_off + L.ks * L.tr * 64 * 4 * 4;
         return;
     }
@@ -894,19 +905,26 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
         L.ks = wide ? 4 : (S2 + 3) / 4;
         L.tr = 2;
         mmq_layout(fmt, S2, false, L);
-        // A 16-column workgroup (one per CU for its LDS) only where all of
-        // them run in one round (Llama-3-8B's 14336-row FFN at 32 columns:
-        // 448 workgroups, 40.2 us, against 8-column ones three to a CU).
-        if (L.mp == 16 && gate->tiles / 2 > (int64_t)ctx->cus * std::max(1, ctx->lds_wide / (L.lds + 2 * L.ks * L.tr * 1024 + 2048))) {
+        // 16-column workgroups: both weights' partial sums of one group
+        // (over the staged codes where they fit there), then h of one group.
+        auto glu16 = [&]() {
+            const int planes_end = mmqt_planes_end(fmt, S2, L), pb = 2 * L.ks * L.tr * 64 * 4 * 4;
+            L.part_off = pb <= L.pl_off ? 0 : planes_end;
+            h_off = L.part_off == 0 ? planes_end : planes_end + pb;
+            L.lds = h_off + 16 * 32 * 4;
+        };
+        if (L.mp == 16) glu16();
+        // A 16-column launch only where all of its workgroups run in one
+        // round (otherwise the 8-column classes, several to a CU).
+        if (L.mp == 16 && gate->tiles / 2 > (int64_t)ctx->cus * std::max(1, ctx->lds_wide / L.lds)) {
             L = mmq_cols(fmt, S2, nc, false);
             L.sbw = 4;
             L.ks = (S2 + 3) / 4;
             L.tr = 2;
             mmq_layout(fmt, S2, false, L);
         }
-        if (L.mp == 16) {  // both weights' partials of one group; h of one group
-            h_off = L.part_off + 2 * L.ks * L.tr * 64 * 4 * 4;
-            L.lds = h_off + 16 * 32 * 4;
+        if (L.mp == 16) {
+            glu16();
         } else {
             h_off = L.part_off + 2 * L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4;  // both weights' partials
             L.lds = h_off + L.g * L.mp * 32 * 4;

@@ -967,6 +967,9 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
         y += C;
     }
     // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
+    // (The fused FFN's partial sums sit over the staged codes: every wave is
+    // done reading them first.)
+    if (GLU) __syncthreads();
     *(v4f*)(part + (wave * 64 + lane) * 4) = y;
     __syncthreads();
     if (!GLU)
@@ -1334,6 +1337,9 @@ __device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
         }
     }
     // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
+    // (The fused FFN's partial sums sit over the staged codes: every wave is
+    // done reading them first.)
+    if (GLU) __syncthreads();
     *(v4f*)(part + (wave * 64 + lane) * 4) = y;
     __syncthreads();
     if (!GLU)
