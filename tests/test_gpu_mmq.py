@@ -71,6 +71,29 @@ def test_mmq_partial_super_blocks(mfma, orc, tname, k):
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
+@pytest.mark.parametrize("k", [1024, 4096, 14336])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9])
+def test_mmq_f32_staging_is_exact(mfma, orc, tname, k, m):
+    """matmul on f32 columns (one column quantized inside the MFMA launch's
+    staging, more quantized once into the scratch first) is bit-identical to
+    matvec on rq_quantize_q8_1 of the same columns, whose codes match the
+    oracle's quantization."""
+    t, n = MMQ_TYPES[tname], 70
+    w = make_weight(orc, t, n, k, 400 + m, "random")
+    wg = upload(mfma, t, w, n, k)
+    x = orc.normal(401 + m + k, m * k, 0.0, 1.0)
+    xd = mfma.from_host(x)
+    got, want = mfma.alloc(m * n), mfma.alloc(m * n)
+    mfma.matmul(xd, wg, got, m)
+    xq = mfma.quantize_q8_1(xd, m, k)
+    qs, d, _ = orc.quantize_q8_1(x, m, k)
+    assert np.array_equal(xq.qs.cpu().numpy(), qs)
+    mfma.matvec(xq, wg, want, m)
+    assert np.array_equal(mfma.to_host(got, m * n).view(np.uint32), mfma.to_host(want, m * n).view(np.uint32))
+    orc.assert_close(f"type {t} {n}x{k} m={m}", orc.matvec_q8_1(t, w, n, k, qs, d, m), mfma.to_host(got, m * n), TOL_B)
+
+
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
 @pytest.mark.parametrize("m", [1, 4])
 def test_mmq_matches_dot4(gpu, orc, tname, m):
     """The same weight in both layouts: identical int32 block dots, f32 sums
