@@ -145,11 +145,11 @@ struct XJ {
 // Raw loads of activation block b of one column: codes, and the f16 scale
 // (parked in ia until prep_x).
 __device__ __forceinline__ void load_x_raw(const int8_t* __restrict__ xq, const u16* __restrict__ xd, int b, XJ& x) {
-    const int4* p = (const int4*)(xq + (int64_t)b * 32);
+    const auto p = gmem((const int4*)(xq + (int64_t)b * 32));
     const int4 lo = p[0], hi = p[1];
     x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
     x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
-    x.ia = xd[b];
+    x.ia = gmem(xd)[b];
 }
 
 // Derived values of one activation block: f32 scale and the code sums the
@@ -261,6 +261,10 @@ __device__ __forceinline__ SBScale sb_scale(const SB<FMT>& w) {
         r.s[1] = (b2 & 0x0F0F0F0Fu) | ((b0 >> 2) & 0x30303030u);
         r.s[2] = b1 & 0x3F3F3F3Fu;
         r.s[3] = ((b2 >> 4) & 0x0F0F0F0Fu) | ((b1 >> 2) & 0x30303030u);
+        // Whole words from here on: each use then selects its byte inside
+        // the instruction (v_cvt_f32_ubyteN, an SDWA byte operand) instead of
+        // a separate bit-field extract that folds the 6-bit mask in.
+        __asm__ volatile("" : "+v"(r.s[0]), "+v"(r.s[1]), "+v"(r.s[2]), "+v"(r.s[3]));
     } else {
         r.d = FMT == RQ_FMT_Q6_K ? h2f(w.tail) : 0.f;
         r.dmin = 0.f;
@@ -279,9 +283,11 @@ template <int FMT>
 __device__ __forceinline__ void sub_accum(const SBScale& sc, int j, const XJ& x, int s0, int s1, float& accd,
                                           float& accm) {
     if (FMT == RQ_FMT_Q4_K) {
+        // sc_j * s0 exactly in int32 (6-bit scale, |s0| < 2^16), then one
+        // rounding: accd += dx * (sc_j * s0).
         const u32 scw = sc.s[j >> 2], mw = sc.s[2 + (j >> 2)];
-        accd += (float)byte_of(scw, j & 3) * (x.dx * (float)s0);
-        accm += (float)byte_of(mw, j & 3) * x.f;
+        accd = fmaf((float)__mul24((int)byte_of(scw, j & 3), s0), x.dx, accd);
+        accm = fmaf((float)byte_of(mw, j & 3), x.f, accm);
     } else if (FMT == RQ_FMT_Q6_K) {
         const u32 w = sc.s[j >> 1];
         const int sc0 = (int)(int8_t)byte_of(w, 2 * (j & 1)), sc1 = (int)(int8_t)byte_of(w, 2 * (j & 1) + 1);
@@ -336,7 +342,7 @@ struct TileLane {
 __device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane, int part = 0) {
     TileLane r;
     if (w.R > 1) {
-        const int sh = __builtin_ctz(64 / w.R);  // log2(Sp)
+        const int sh = 6 - __builtin_ctz(w.R);  // log2(Sp): R is a power of two
         r.row = lane >> sh;
         r.col = lane & ((1 << sh) - 1);
         r.real = r.col < w.S;
@@ -351,7 +357,7 @@ __device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane, int pa
 }
 
 // Lanes per row group: Sp when R > 1, else the wave.
-__device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? 64 / w.R : 64; }
+__device__ __forceinline__ int row_group(const RqTiled& w) { return w.R > 1 ? 64 >> __builtin_ctz(w.R) : 64; }
 
 // Where a lane's row sum goes: worked out before the weights arrive, so the
 // tail of the wave is the reduction and one store.
@@ -468,8 +474,8 @@ struct QItem {
 __device__ __forceinline__ void qitem_load(const float* __restrict__ xf, int k, int total, int S, int U, int base,
                                            QItem& q) {
     q.si = stage_item<1>(base + (threadIdx.x >> 2), total, S, U);
-    const float4* p = (const float4*)(xf + (int64_t)q.si.col * k + (int64_t)(q.si.valid ? q.si.b : 0) * 32 +
-                                      8 * (threadIdx.x & 3));
+    const auto p = gmem((const float4*)(xf + (int64_t)q.si.col * k + (int64_t)(q.si.valid ? q.si.b : 0) * 32 +
+                                        8 * (threadIdx.x & 3)));
     const float4 a = p[0], b = p[1];
     q.v[0] = a.x; q.v[1] = a.y; q.v[2] = a.z; q.v[3] = a.w;
     q.v[4] = b.x; q.v[5] = b.y; q.v[6] = b.z; q.v[7] = b.w;
@@ -663,6 +669,12 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // By value (a reference indexed by ti reloads its fields with dependent
     // scalar loads at each use).
     const RqMvTarget T = pick_target(P, ti);
+    // The activation pointers join the first batch of kernarg loads (used
+    // only in the staging, they were otherwise fetched in a second round
+    // trip after the target pick, in front of every load of the wave).
+    const int8_t* xq = F32IN ? nullptr : sgpr_value(P.xq);
+    const u16* xd = F32IN ? nullptr : sgpr_value(P.xd);
+    const float* xf = F32IN ? sgpr_value(P.xf) : nullptr;
     // Rows wider than 64 super-blocks (R = 1) are split over kp = 2 or 4
     // waves of one workgroup: wave `part` of a tile takes super-blocks 64
     // part .. 64 part + 63 (then every 64 kp-th further on), all loaded up
@@ -682,7 +694,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
     constexpr bool ORDER = NC == 1 && !KP && FMT != RQ_FMT_Q8_0;
-    stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
+    stage_columns<FMT, NC, F32IN, WAVES>(xq, xd, xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
     if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
 
     float acc[NC];
