@@ -1561,7 +1561,7 @@ extern "C" rq_status rq_weight_to_gguf(rq_ctx* ctx, const rq_weight* w, void* gg
                     const int sh = (j & 1) * 4;
                     for (int i = 0; i < 16; i++) {
                         q[i] |= (uint8_t)((v[i] & 0xF) << sh);
-                        q[i + 16] |= (uint8_t)((v[i] >> 4) << sh);
+                        q[i + 16] |= (uint8_t)(((v[i] >> 4) ^ 8) << sh);  // stored XOR 8
                     }
                 }
             } else if (w->fmt == RQ_FMT_Q6_K) {
@@ -1590,7 +1590,8 @@ extern "C" rq_status rq_weight_to_gguf(rq_ctx* ctx, const rq_weight* w, void* gg
                     b[0] = dv[2 * j];
                     b[1] = dv[2 * j + 1];
                     if (w->fmt == RQ_FMT_Q4_0) {
-                        memcpy(b + 2, chunk(1 + j), 16);
+                        const uint8_t* v = chunk(1 + j);
+                        for (int i = 0; i < 16; i++) b[2 + i] = (uint8_t)(v[i] ^ 0x80);  // high nibble stored XOR 8
                     } else {
                         memcpy(b + 2, chunk(1 + 2 * j), 16);
                         memcpy(b + 18, chunk(2 + 2 * j), 16);

@@ -138,8 +138,8 @@ struct XJ {
     int q[8];  // 32 int8 codes
     float dx;  // f32 of the stored f16 scale
     float f;   // Q4_K: dx * sum(q)
-    int ia;    // Q4_0: -8 * sum(q); Q6_K: -32 * sum(q[0..15])
-    int ib;    // Q6_K: -32 * sum(q[16..31])
+    int ia;    // Q4_0: -8 * sum(q[0..15]); Q6_K: -32 * sum(q[0..15])
+    int ib;    // Q4_K: 128 * sum(q[16..31]); Q6_K: -32 * sum(q[16..31])
 };
 
 // Raw loads of activation block b of one column: codes, and the f16 scale
@@ -172,7 +172,8 @@ __device__ __forceinline__ void prep_x(XJ& x, bool valid) {
             sa = dot4(x.q[i], 0x01010101, sa);
             sb = dot4(x.q[4 + i], 0x01010101, sb);
         }
-        if (FMT == RQ_FMT_Q4_0) x.ia = -8 * (sa + sb);
+        if (FMT == RQ_FMT_Q4_0) x.ia = -8 * sa;
+        if (FMT == RQ_FMT_Q4_K) x.ib = 128 * sb;
         if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K) x.f = x.dx * (float)(sa + sb);
         if (FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K) {
             x.ia = -32 * sa;
@@ -183,12 +184,13 @@ __device__ __forceinline__ void prep_x(XJ& x, bool valid) {
 
 // ---------------------------------------------------------------------------
 // Integer block dots of sub-block j (shared by the matvecs and the debug
-// dots kernel). Q8_0: s0 = sum q*x. Q4_0: s0 = sum (q-8)*x. Q4_K: s0 =
-// sum q*x (q in 0..15; the min term uses the activation sum). Q6_K: s0, s1 =
-// sum (q-32)*x over elements 0..15 and 16..31 of the sub-block. The code
+// dots kernel). Q8_0: s0 = sum q*x. Q4_0: s0 = 16 sum (q-8)*x. Q4_K: s0 =
+// 16 sum q*x (q in 0..15; the min term uses the activation sum). Q6_K: s0,
+// s1 = sum (q-32)*x over elements 0..15 and 16..31 of the sub-block. The code
 // offsets enter as the chain's start value: sum (q-c)*x = -c*sum x + sum q*x.
+// MIXREC: x is a record of a mixed Q4_K / Q6_K launch (ib = -32 sum(q[16..31])).
 
-template <int FMT>
+template <int FMT, bool MIXREC = false>
 __device__ __forceinline__ void sub_dot(const SB<FMT>& w, int j, const XJ& x, int& s0, int& s1) {
     if (FMT == RQ_FMT_Q8_0) {
         const int4 a = w.c[1 + 2 * j], b = w.c[2 + 2 * j];
@@ -204,20 +206,26 @@ __device__ __forceinline__ void sub_dot(const SB<FMT>& w, int j, const XJ& x, in
         s1 = 0;
     } else if (FMT == RQ_FMT_Q4_0 || FMT == RQ_FMT_Q4_K) {
         const int4 v = w.c[1 + j];
-        // low nibbles: elements 0..15; high nibbles (one 64-bit shift per
-        // pair of dwords): elements 16..31
-        const u64 v01 = (u64)(u32)v.x | ((u64)(u32)v.y << 32), v23 = (u64)(u32)v.z | ((u64)(u32)v.w << 32);
-        const u64 h01 = (v01 >> 4) & 0x0F0F0F0F0F0F0F0Full, h23 = (v23 >> 4) & 0x0F0F0F0F0F0F0F0Full;
-        int s = FMT == RQ_FMT_Q4_0 ? x.ia : 0;
-        s = dot4((int)((u32)v.x & 0x0F0F0F0Fu), x.q[0], s);
-        s = dot4((int)((u32)v.y & 0x0F0F0F0Fu), x.q[1], s);
-        s = dot4((int)((u32)v.z & 0x0F0F0F0Fu), x.q[2], s);
-        s = dot4((int)((u32)v.w & 0x0F0F0F0Fu), x.q[3], s);
-        s = dot4((int)(u32)h01, x.q[4], s);
-        s = dot4((int)(u32)(h01 >> 32), x.q[5], s);
-        s = dot4((int)(u32)h23, x.q[6], s);
-        s = dot4((int)(u32)(h23 >> 32), x.q[7], s);
-        s0 = s;
+        // Low nibbles: codes of elements 0..15 (0..15). High nibbles, stored
+        // XOR 8: masked in place with 0xF0, each byte is the signed 16 (q - 8)
+        // of elements 16..31, so neither half needs a shift. a = sum (q - c) x
+        // over 0..15, b = 16 sum (q - c) x over 16..31 (c = 8 for Q4_0; for
+        // Q4_K, c = 0 through b's start value 128 sum x), s0 = 16 a + b.
+        int a = FMT == RQ_FMT_Q4_0 ? x.ia : 0;
+        int b = FMT == RQ_FMT_Q4_K ? (MIXREC ? -4 * x.ib : x.ib) : 0;
+        a = dot4((int)((u32)v.x & 0x0F0F0F0Fu), x.q[0], a);
+        a = dot4((int)((u32)v.y & 0x0F0F0F0Fu), x.q[1], a);
+        a = dot4((int)((u32)v.z & 0x0F0F0F0Fu), x.q[2], a);
+        a = dot4((int)((u32)v.w & 0x0F0F0F0Fu), x.q[3], a);
+        b = dot4((int)((u32)v.x & 0xF0F0F0F0u), x.q[4], b);
+        b = dot4((int)((u32)v.y & 0xF0F0F0F0u), x.q[5], b);
+        b = dot4((int)((u32)v.z & 0xF0F0F0F0u), x.q[6], b);
+        b = dot4((int)((u32)v.w & 0xF0F0F0F0u), x.q[7], b);
+        s0 = 16 * a + b;
+        // Opaque from here: the multiply by the scale byte (v_mul_i32_i24)
+        // then takes it as it is, instead of the compiler re-deriving its
+        // low 24 bits with two extra shifts.
+        __asm__("" : "+v"(s0));
         s1 = 0;
     } else {  // Q6_K
         const int4 lo = w.c[1 + j];
@@ -283,8 +291,8 @@ template <int FMT>
 __device__ __forceinline__ void sub_accum(const SBScale& sc, int j, const XJ& x, int s0, int s1, float& accd,
                                           float& accm) {
     if (FMT == RQ_FMT_Q4_K) {
-        // sc_j * s0 exactly in int32 (6-bit scale, |s0| < 2^16), then one
-        // rounding: accd += dx * (sc_j * s0).
+        // sc_j * s0 exactly in int32 (6-bit scale, |s0| < 2^20, a multiple of
+        // 16), then one rounding: accd += dx * (sc_j * s0).
         const u32 scw = sc.s[j >> 2], mw = sc.s[2 + (j >> 2)];
         accd = fmaf((float)__mul24((int)byte_of(scw, j & 3), s0), x.dx, accd);
         accm = fmaf((float)byte_of(mw, j & 3), x.f, accm);
@@ -298,10 +306,14 @@ __device__ __forceinline__ void sub_accum(const SBScale& sc, int j, const XJ& x,
     }
 }
 
+// The Q4 formats' dots are 16 times the block dots; every term of accd then
+// is exactly 16 times its value, and the factor leaves exactly here (d / 16
+// and accd / 16 are exact scalings by a power of two).
 template <int FMT>
 __device__ __forceinline__ float sb_finish(const SBScale& sc, float accd, float accm) {
-    if (FMT == RQ_FMT_Q4_K) return sc.d * accd - sc.dmin * accm;
+    if (FMT == RQ_FMT_Q4_K) return (sc.d * 0.0625f) * accd - sc.dmin * accm;
     if (FMT == RQ_FMT_Q6_K) return sc.d * accd;
+    if (FMT == RQ_FMT_Q4_0) return accd * 0.0625f;
     return accd;
 }
 
@@ -512,8 +524,8 @@ __device__ __forceinline__ void qitem_write(QItem& q, int S) {
             m.dx = h2f(f2h(d));
             const bool k4 = FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K, k6 = FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K;
             m.f = k4 ? m.dx * (float)(sa + sb) : 0.f;
-            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * (sa + sb) : (k6 ? -32 * sa : 0);
-            m.ib = k6 ? -32 * sb : 0;
+            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * sa : (k6 ? -32 * sa : 0);
+            m.ib = FMT == RQ_FMT_Q4_K ? 128 * sb : (k6 ? -32 * sb : 0);
             *(XMeta*)(rec + 256 + 16 * q.si.j) = m;
         }
     }
@@ -538,7 +550,7 @@ __device__ __forceinline__ void pin_sub(SB<FMT>& w, int j) {
 }
 
 // Dot of one super-block slot with nc columns, accumulated into acc.
-template <int FMT, int NC>
+template <int FMT, int NC, bool MIXREC = false>
 __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool active, float* acc) {
     const SBScale sc = sb_scale<FMT>(w);
 #pragma unroll
@@ -563,7 +575,7 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
                 if (j < 7) lds_read_x(rec, j + 1, xn);
                 pin_sub<FMT>(wp, j);
                 int s0, s1;
-                sub_dot<FMT>(wp, j, x, s0, s1);
+                sub_dot<FMT, MIXREC>(wp, j, x, s0, s1);
                 sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
                 __asm__ volatile("" : "+v"(accd), "+v"(accm));
             }
@@ -573,7 +585,7 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
                 XJ x;
                 lds_read_x(rec, j, x);
                 int s0, s1;
-                sub_dot<FMT>(w, j, x, s0, s1);
+                sub_dot<FMT, MIXREC>(w, j, x, s0, s1);
                 sub_accum<FMT>(sc, j, x, s0, s1, accd, accm);
             }
         }
@@ -798,10 +810,13 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
 #pragma unroll
             for (int c = 0; c < Fmt<RQ_FMT_Q4_K>::C; c++) w4.c[c] = w.c[c];
             w4.tail = 0u;
-            slot_dot<RQ_FMT_Q4_K, NC>(w4, S, a, active, acc);
+            slot_dot<RQ_FMT_Q4_K, NC, true>(w4, S, a, active, acc);
         }
     };
-    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
+    const int8_t* xq = F32IN ? nullptr : sgpr_value(P.xq);  // first kernarg batch (as mvx_body)
+    const u16* xd = F32IN ? nullptr : sgpr_value(P.xd);
+    const float* xf = F32IN ? sgpr_value(P.xf) : nullptr;
+    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(xq, xd, xf, S, k,
                                                   [&] { load(has_tile ? t : T.w.T - 1, tl.slot); });
     if (!has_tile) return;
 
@@ -1076,7 +1091,7 @@ __device__ __forceinline__ void dots_body(const RqDotsParams& p) {
                 out[2 * b] = s0;
                 out[2 * b + 1] = s1;
             } else {
-                out[b] = s0;
+                out[b] = FMT == RQ_FMT_Q8_0 ? s0 : s0 >> 4;  // Q4: 16 x the dot, exactly
             }
         }
     }
@@ -1124,7 +1139,8 @@ __device__ __forceinline__ void repack_body(const RqRepackParams& p) {
             // sub-block j: chunk j/2 of 32 bytes, low (j even) or high nibbles
             const u8* q = b + 16 + (j >> 1) * 32;
             const int sh = (j & 1) * 4;
-            for (int i = 0; i < 16; i++) v[i] = (u8)(((q[i] >> sh) & 0xF) | (((q[i + 16] >> sh) & 0xF) << 4));
+            for (int i = 0; i < 16; i++)
+                v[i] = (u8)(((q[i] >> sh) & 0xF) | ((((q[i + 16] >> sh) & 0xF) ^ 8) << 4));
             st16(base + (1 + j) * cstride, v);
         }
     } else if (FMT == RQ_FMT_Q6_K) {
@@ -1167,7 +1183,8 @@ __device__ __forceinline__ void repack_body(const RqRepackParams& p) {
                 dv[2 * j] = b[0];
                 dv[2 * j + 1] = b[1];
                 if (FMT == RQ_FMT_Q4_0) {
-                    st16(base + (1 + j) * cstride, b + 2);
+                    for (int i = 0; i < 16; i++) v[i] = (u8)(b[2 + i] ^ 0x80);  // high nibble XOR 8
+                    st16(base + (1 + j) * cstride, v);
                 } else {
                     st16(base + (1 + 2 * j) * cstride, b + 2);
                     st16(base + (2 + 2 * j) * cstride, b + 18);

@@ -16,9 +16,11 @@
 // so each of a wave's chunk loads is one contiguous run of 16 B per lane.
 //
 //   Q4_K  C = 9   c0: GGUF d, dmin and packed 6-bit scales/mins, verbatim
-//                 c1+j: sub-block j (32 elements), byte b = q[b] | q[b+16] << 4
+//                 c1+j: sub-block j (32 elements), byte b = q[b] | (q[b+16] ^ 8) << 4
+//                       (the high nibble XOR 8: masked with 0xF0 it reads as
+//                       the signed byte 16 (q[b+16] - 8))
 //   Q4_0  C = 9   c0: the eight blocks' f16 d
-//                 c1+j: block j's 16 bytes in GGUF order (same nibble rule)
+//                 c1+j: block j's 16 GGUF bytes with the high nibbles XOR 8
 //   Q8_0  C = 17  c0: the eight blocks' f16 d
 //                 c1+2j+h: block j's codes 16h .. 16h+15
 //   Q6_K  C = 13  c0: the 16 int8 sub-scales (GGUF bytes 192..207)
