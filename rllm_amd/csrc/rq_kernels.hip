@@ -152,6 +152,29 @@ __device__ __forceinline__ void load_x_raw(const int8_t* __restrict__ xq, const 
     x.ia = gmem(xd)[b];
 }
 
+// The per-block values a record carries besides the codes, from the f32
+// scale dx and the code sums sa (codes 0..15) and sb (16..31).
+struct XMeta {
+    float dx, f;
+    int ia, ib;
+};
+
+template <int FMT>
+__device__ __forceinline__ XMeta x_meta(float dx, int sa, int sb) {
+    XMeta m;
+    m.dx = dx;
+    m.f = FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K ? dx * (float)(sa + sb) : 0.f;
+    const bool k6 = FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K;
+    m.ia = FMT == RQ_FMT_Q4_0 ? -8 * sa : (k6 ? -32 * sa : 0);
+    m.ib = FMT == RQ_FMT_Q4_K ? 128 * sb : (k6 ? -32 * sb : 0);
+    return m;
+}
+
+// Sum of the 16 signed codes of four packed dwords.
+__device__ __forceinline__ int code_sum16(int a, int b, int c, int d) {
+    return dot4(d, 0x01010101, dot4(c, 0x01010101, dot4(b, 0x01010101, dot4(a, 0x01010101, 0))));
+}
+
 // Derived values of one activation block: f32 scale and the code sums the
 // offset and min terms need. valid == false zeroes the block.
 template <int FMT>
@@ -161,25 +184,14 @@ __device__ __forceinline__ void prep_x(XJ& x, bool valid) {
         for (int i = 0; i < 8; i++) x.q[i] = 0;
         x.ia = 0;
     }
-    x.dx = h2f((u32)x.ia);
-    x.f = 0.f;
-    x.ia = 0;
-    x.ib = 0;
-    if (FMT != RQ_FMT_Q8_0) {
-        int sa = 0, sb = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            sa = dot4(x.q[i], 0x01010101, sa);
-            sb = dot4(x.q[4 + i], 0x01010101, sb);
-        }
-        if (FMT == RQ_FMT_Q4_0) x.ia = -8 * sa;
-        if (FMT == RQ_FMT_Q4_K) x.ib = 128 * sb;
-        if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K) x.f = x.dx * (float)(sa + sb);
-        if (FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K) {
-            x.ia = -32 * sa;
-            x.ib = -32 * sb;
-        }
-    }
+    const float dx = h2f((u32)x.ia);
+    const int sa = FMT == RQ_FMT_Q8_0 ? 0 : code_sum16(x.q[0], x.q[1], x.q[2], x.q[3]);
+    const int sb = FMT == RQ_FMT_Q8_0 ? 0 : code_sum16(x.q[4], x.q[5], x.q[6], x.q[7]);
+    const XMeta m = x_meta<FMT>(dx, sa, sb);
+    x.dx = m.dx;
+    x.f = m.f;
+    x.ia = m.ia;
+    x.ib = m.ib;
 }
 
 // ---------------------------------------------------------------------------
@@ -410,11 +422,6 @@ __device__ __forceinline__ void tile_store(const RowDst& d, int64_t n, float v, 
 
 #define RQ_LDS_REC 400
 
-struct XMeta {
-    float dx, f;
-    int ia, ib;
-};
-
 __device__ __forceinline__ char* lds_rec(char* base, int S, int col, int s) {
     return base + ((size_t)col * S + s) * RQ_LDS_REC;
 }
@@ -471,6 +478,46 @@ __device__ __forceinline__ void stage_write(const StageItem& si, XJ& x, int S) {
     }
 }
 
+// Staging by halves (the plain matvecs, stage_columns' HALVES): when a
+// workgroup's threads outnumber twice its blocks, thread h stages the 16-byte
+// half h % 2 of block item h / 2 (one code load and one scale load per thread,
+// against three loads for each of two items), the two halves' code sums meet
+// across the lane pair, and the even lane writes the block's per-block
+// values. Every lane of the wave must be active. (Q4_K 14336 x 4096, one
+// column: 6.947 -> 6.906 us. In the gated-FFN kernel the compiler then waited
+// for all weight loads before the staging barrier: 13.6 -> 14.2 us, so that
+// one keeps the item staging.)
+struct XHalf {
+    StageItem si;
+    int4 q;
+    u32 d16;
+};
+
+template <int NC>
+__device__ __forceinline__ void xhalf_load(const int8_t* xq, const u16* xd, int k, int total, int S, int U,
+                                           XHalf& h) {
+    h.si = stage_item<NC>(threadIdx.x >> 1, total, S, U);
+    const int b = h.si.valid ? h.si.b : 0;
+    h.q = gmem((const int4*)(xq + (int64_t)h.si.col * k + (int64_t)b * 32 + 16 * (threadIdx.x & 1)))[0];
+    h.d16 = gmem(xd + (int64_t)h.si.col * U)[b];
+}
+
+template <int FMT>
+__device__ __forceinline__ void xhalf_write(XHalf& h, int S) {
+    const bool hi = threadIdx.x & 1;
+    if (!h.si.valid) {
+        h.q = make_int4(0, 0, 0, 0);
+        h.d16 = 0;
+    }
+    const int s = FMT == RQ_FMT_Q8_0 ? 0 : code_sum16(h.q.x, h.q.y, h.q.z, h.q.w);
+    const int other = dpp_i<DPP_QUAD_1032>(s);  // the pair's other half
+    if (h.si.store) {
+        char* rec = lds_rec(rq_lds, S, h.si.col, h.si.s);
+        *(int4*)(rec + 32 * h.si.j + 16 * hi) = h.q;
+        if (!hi) *(XMeta*)(rec + 256 + 16 * h.si.j) = x_meta<FMT>(h2f(h.d16), s, other);
+    }
+}
+
 // Staging from f32 activations (the fused quantize of rq_matmul): four lanes
 // (a quad) per 32-value block, eight values each; amax and the code sums meet
 // across the quad with DPP. The arithmetic is rq_quantize_q8_1's (q8_codes,
@@ -518,16 +565,7 @@ __device__ __forceinline__ void qitem_write(QItem& q, int S) {
         c.x = (qv[0] & 0xFF) | ((qv[1] & 0xFF) << 8) | ((qv[2] & 0xFF) << 16) | ((qv[3] & 0xFF) << 24);
         c.y = (qv[4] & 0xFF) | ((qv[5] & 0xFF) << 8) | ((qv[6] & 0xFF) << 16) | ((qv[7] & 0xFF) << 24);
         *(int2*)(rec + 32 * q.si.j + 8 * ql) = c;
-        if (ql == 0) {
-            const int sa = pair, sb = other;
-            XMeta m;
-            m.dx = h2f(f2h(d));
-            const bool k4 = FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_MIX_K, k6 = FMT == RQ_FMT_Q6_K || FMT == RQ_FMT_MIX_K;
-            m.f = k4 ? m.dx * (float)(sa + sb) : 0.f;
-            m.ia = FMT == RQ_FMT_Q4_0 ? -8 * sa : (k6 ? -32 * sa : 0);
-            m.ib = FMT == RQ_FMT_Q4_K ? 128 * sb : (k6 ? -32 * sb : 0);
-            *(XMeta*)(rec + 256 + 16 * q.si.j) = m;
-        }
+        if (ql == 0) *(XMeta*)(rec + 256 + 16 * q.si.j) = x_meta<FMT>(h2f(f2h(d)), pair, other);
     }
 }
 
@@ -599,7 +637,7 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
 // caller's weight loads), then the LDS writes, which wait only for the
 // staging loads issued before the weights, then the remaining rounds and a
 // barrier. Activations are Q8_1 (xq, xd) or, with F32IN, f32 quantized here.
-template <int FMT, int NC, bool F32IN, int WAVES, class LoadW>
+template <int FMT, int NC, bool F32IN, int WAVES, bool HALVES = false, class LoadW>
 __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, const float* xf, int S, int k,
                                               LoadW&& load_w) {
     constexpr int THREADS = 64 * WAVES, QITEMS = THREADS / 4;
@@ -621,6 +659,13 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
             qitem_load(xf, k, total, S, U, base, q);
             qitem_write<FMT>(q, S);
         }
+    } else if (HALVES && 2 * total <= THREADS) {
+        // One round of halves (see XHalf), loaded before the weights.
+        XHalf h;
+        xhalf_load<NC>(xq, xd, k, total, S, U, h);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);
+        xhalf_write<FMT>(h, S);
     } else {
         // Every thread loads two items (clamped to the last one past the end:
         // cache hits), unconditionally: loads under a branch made the
@@ -706,7 +751,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
     constexpr bool ORDER = NC == 1 && !KP && FMT != RQ_FMT_Q8_0;
-    stage_columns<FMT, NC, F32IN, WAVES>(xq, xd, xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
+    stage_columns<FMT, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
     if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
 
     float acc[NC];
@@ -792,14 +837,23 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const RowDst dst = row_dst(T, t, lane);
 
     SB<RQ_FMT_Q6_K> w;  // Q4_K: chunks 0..8
+    // Chunk c of a slot lies at the same offset from the tile's start in
+    // both formats (only the chunk count C differs), so chunks 0..8 are one
+    // load sequence for either; Q6_K's chunks 9..12 and scale follow under
+    // the branch. (With the whole load under an if / else, the structurized
+    // control flow made the Q6_K path wait for every staging load before its
+    // first weight load.)
     auto load = [&](int tt, int a) {
-        if (q6) {
-            load_sb<RQ_FMT_Q6_K>(T.w, tt, a, w);
-        } else {
-            SB<RQ_FMT_Q4_K> w4;
-            load_sb<RQ_FMT_Q4_K>(T.w, tt, a, w4);
+        const int64_t slots = (int64_t)T.w.R * S;
+        const u8* base = T.w.main + ((int64_t)tt * (q6 ? 13 : 9) * slots + a) * 16;
 #pragma unroll
-            for (int c = 0; c < Fmt<RQ_FMT_Q4_K>::C; c++) w.c[c] = w4.c[c];
+        for (int c = 0; c < Fmt<RQ_FMT_Q4_K>::C; c++) w.c[c] = ld16_nt(base + (int64_t)c * slots * 16);
+        w.tail = 0u;
+        if (q6) {
+#pragma unroll
+            for (int c = Fmt<RQ_FMT_Q4_K>::C; c < Fmt<RQ_FMT_Q6_K>::C; c++)
+                w.c[c] = ld16_nt(base + (int64_t)c * slots * 16);
+            w.tail = (u32) * gmem((const u16*)(T.w.tail + ((int64_t)tt * slots + a) * 2));
         }
     };
     auto dot = [&](int a, bool active, float* acc) {
