@@ -10,6 +10,8 @@
 // with XOR, reduces them over each row's lane group with the same DPP steps
 // and stores one 4-byte word per row, as the matvec stores one f32 per row.
 // Its time is what a launch of that shape costs for its memory traffic alone.
+// rq_floor_empty launches the same grid with no work at all: the fixed cost
+// of one dependent launch in a replayed graph.
 
 #include "rq_device.h"
 
@@ -53,5 +55,15 @@ extern "C" int rq_floor_read(const void* base, int64_t tiles, int chunks, int la
     case 17: hipLaunchKernelGGL(rq_floor_read_k<17>, grid, block, 0, s, b, tiles, lanes_per_row, (u32*)out, rows); break;
     default: return (int)hipErrorInvalidValue;
     }
+    return (int)hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void rq_floor_empty_k() {}
+
+// Launches `workgroups` empty 256-thread workgroups on `stream`. Returns a
+// hipError_t.
+extern "C" int rq_floor_empty(int64_t workgroups, void* stream) {
+    if (workgroups <= 0 || workgroups > 0x7fffffff) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rq_floor_empty_k, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream);
     return (int)hipGetLastError();
 }
