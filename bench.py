@@ -245,6 +245,30 @@ def bench_cold(torch, gpu, orc, t, n, k, reps=7, seed=7):
     return statistics.median(times)
 
 
+def bench_qkv(torch, gpu, orc, steps, warmup):
+    """The decode step's q/k/v: q 4096x4096 and k 1024x4096 in Q4_K, v
+    1024x4096 in Q6_K, one matvec_many launch on a Q8_1 column (rotating
+    weight copies), per launch."""
+    shapes = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096)]
+    hosts = [make_gguf(orc, t, n, k, 80 + i) for i, (t, n, k) in enumerate(shapes)]
+    copies = rotation_copies(sum(h.nbytes for h in hosts))
+    ws = [upload_copies(gpu, t, n, k, h, copies) for (t, n, k), h in zip(shapes, hosts)]
+    xq = gpu.quantize_q8_1(gpu.from_host(orc.normal(83, 4096, 0.0, 1.0)), 1, 4096)
+    outs = [gpu.alloc(n) for _, n, _ in shapes]
+    chunk = max(1, 256 // copies) * copies
+    per, g = time_graph(torch, gpu, lambda i: gpu.matvec_many(xq, [w[i % copies] for w in ws], outs, 1), chunk, steps,
+                        warmup)
+    del g
+    for wl in ws:
+        for w in wl:
+            w.free()
+    torch.cuda.synchronize()
+    per_launch = [p / chunk for p in per]
+    us = statistics.median(per_launch)
+    b = sum(alg_bytes(t, n, k, 1) for t, n, k in shapes)
+    return {"us": us, "spread": spread(per_launch), "gbs": b / us / 1e3, "bytes": b}
+
+
 def bench_ffn(torch, gpu, orc, steps, warmup, m=1):
     """BASELINE config 3 as the decode step runs it: gated_ffn (gate/up
     Q4_K 14336 x 4096 fused with SiLU and the product's Q8_1, down Q6_K
@@ -647,6 +671,17 @@ def main() -> int:
             log(f"{label} {n}x{k} m={m} ({c['kernels']}): {c['us']:.2f} us, {c['gbs']:.0f} GB/s "
                 f"({100 * c['gbs'] / HBM_PEAK_GBS:.1f}%)")
             configs.append(config_line(label, c, t, n, k, m))
+        # The decode step's two small launches, per launch (attn_output; q/k/v
+        # as one mixed launch), beside their read floor (launch_floors_us).
+        c = bench_matvec(torch, gpu, orc, 12, 4096, 4096, 1, cfg_steps, cfg_warm)
+        log(f"decode launch: attn_output Q4_K 4096x4096 m=1: {c['us']:.2f} us, {c['gbs']:.0f} GB/s")
+        configs.append(config_line("decode launch: attn_output Q4_K", c, 12, 4096, 4096, 1))
+        c = bench_qkv(torch, gpu, orc, cfg_steps, cfg_warm)
+        log(f"decode launch: q/k/v (Q4_K 4096x4096 + 1024x4096, Q6_K 1024x4096) m=1: {c['us']:.2f} us, "
+            f"{c['gbs']:.0f} GB/s")
+        configs.append({"config": "decode launch: q/k/v in one launch (Q4_K 4096x4096 + 1024x4096, Q6_K 1024x4096)",
+                        "batch": 1, "us": round(c["us"], 3), "spread_us": c["spread"], "GB_s": round(c["gbs"], 1),
+                        "pct_hbm_peak": round(100 * c["gbs"] / HBM_PEAK_GBS, 1)})
         f = bench_ffn(torch, gpu, orc, cfg_steps, cfg_warm)
         log(f"config 3: gated FFN 14336/4096 m=1: {f['us']:.2f} us, {f['gbs']:.0f} GB/s")
         configs.append({"config": "config 3: gated FFN (gate/up Q4_K 14336x4096 + SiLU + Q8_1, down Q6_K 4096x14336)",
