@@ -694,11 +694,19 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 // (rq_mmq_<fmt>_16x<g>_<sbw>: up to 16 g columns per launch, staged 16 at a
 // time against weights read once into registers). A D entry is the exact
 // int32 dot of one 32-element block of the lane's weight row n with one
-// activation. The A operand's rows are the group's 16 activations, one
-// 16-byte LDS read per lane and window (all lanes: k-group g of activation
-// lane % 16); each window takes two MFMAs, one per block h, whose B operand
-// is the weight window with the other block's k-groups zeroed (a lane mask
-// folded into the nibble mask). Lane (g, n)'s entries are then block 2w + h,
+// activation. The A operand's rows are the group's 16 activations; each
+// window takes two MFMAs, one per block h. With AMASK (Q4_K, Q8_0: one
+// column group, or two of Q8_0 at 2 super-blocks per wave) B is the whole
+// weight window and A register set h holds the
+// window's codes in the lanes of block h's k-groups (g / 2 == h) and zeros in
+// the others: a lane refreshes only its own set, with one exec-masked
+// 16-byte LDS read per window, so the block selection costs no VALU.
+// Otherwise (the classes whose registers have no room for the second set:
+// Q4_K 16 x 2 at 4 super-blocks per wave spilled 76; and Q4_0, whose
+// 16-column launch it made slower: 4096 x 4096 at 16 columns 6.92 -> 7.35 us)
+// A is one full read and B is the
+// window with the other block's k-groups zeroed, a lane mask folded into the
+// nibble mask. Lane (g, n)'s entries are then block 2w + h,
 // activations 4g .. 4g + 3: the row's scales serve all four, and their
 // activation scales are one 16-byte LDS read per window (f16, both blocks).
 // Per entry the scaling is three VALU instructions: sc * D in int32 (Q4_K;
@@ -869,15 +877,19 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
     u32 ksc[SBW][2];
     float kd[SBW];
     float cb4[SBW][2];
-    // B masks of MFMA h: the nibble (or byte) mask where the lane's k-group
-    // lies in block h, else 0 (mk[window parity][h]).
+    constexpr bool AMASK = FMT != RQ_FMT_Q4_0 && (G == 1 || (FMT == RQ_FMT_Q8_0 && G == 2 && SBW == 2 && !GLU));
+    // AMASK: A register sets of blocks 0 and 1 of a window; a lane only ever
+    // writes the one of its own block (g / 2), so the other stays zero.
+    // Otherwise the B masks of MFMA h: the nibble (or byte) mask where the
+    // lane's k-group lies in block h, else 0 (mk[window parity][h]).
+    v4i Ah[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
     u32 mk[2][2];
 #pragma unroll
     for (int par = 0; par < 2; par++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const u32 m = NIB ? (par ? 0xF0F0F0F0u : 0x0F0F0F0Fu) : 0xFFFFFFFFu;
-            mk[par][h] = (g >> 1) == h ? m : 0u;
+            mk[par][h] = AMASK || (g >> 1) == h ? m : 0u;
         }
 
     const char* dxp = mmq_lds + P.pl_off;                          // f16 dx, [block pair][16][2]
@@ -930,14 +942,29 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 const int4 v = NIB ? wv[i * 2 + (w >> 1)] : wv[i * 4 + w];
-                const v4i A = lds16(xoff + 256 * i + 64 * w);
+                v4i A;
+                if (AMASK) {
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        if ((g >> 1) == h) Ah[h] = lds16(xoff + 256 * i + 64 * w);
+                } else {
+                    A = lds16(xoff + 256 * i + 64 * w);
+                }
                 // dx of activations a4 .. a4 + 3 (dwords), blocks 2w (low halves) and 2w + 1
                 const int4 dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
+                v4i B;
+                if (AMASK) {
+                    const u32 m = mk[NIB ? (w & 1) : 0][0];
+                    B = NIB ? v4i{(int)((u32)v.x & m), (int)((u32)v.y & m), (int)((u32)v.z & m), (int)((u32)v.w & m)}
+                            : v4i{v.x, v.y, v.z, v.w};
+                }
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const u32 m = mk[NIB ? (w & 1) : 0][h];
-                    const v4i B = v4i{(int)((u32)v.x & m), (int)((u32)v.y & m), (int)((u32)v.z & m), (int)((u32)v.w & m)};
-                    const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i{0, 0, 0, 0}), 0, 0, 0);
+                    if (!AMASK) {
+                        const u32 m = mk[NIB ? (w & 1) : 0][h];
+                        B = v4i{(int)((u32)v.x & m), (int)((u32)v.y & m), (int)((u32)v.z & m), (int)((u32)v.w & m)};
+                    }
+                    const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(AMASK ? Ah[h] : A, B, (v4i{0, 0, 0, 0}), 0, 0, 0);
                     const u32 dxv[4] = {(u32)dxw.x, (u32)dxw.y, (u32)dxw.z, (u32)dxw.w};
                     const int b = 2 * w + h;  // block within the super-block
                     v4f& ac = acc[NIB ? (w & 1) : 0];
