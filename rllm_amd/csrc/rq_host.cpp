@@ -627,7 +627,15 @@ int mmqt_g_index(int g) { return g == 1 ? 0 : g == 2 ? 1 : 2; }
 // Q8_0, whose per-block scales (and Q8_0's 64 registers of codes at 4) would
 // not fit the 128 registers of a 1024-thread workgroup's waves with 4,
 // unless the row is too wide for 16 waves of 2.
-int mmqt_sbw(int fmt, int S2) { return fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q6_K || (S2 + 1) / 2 > 16 ? 4 : 2; }
+// Super-blocks per wave of the 16-column classes. Q4_K takes 2 in launches
+// of at most kMmqtSmallTiles tiles (twice the waves where one per SIMD would
+// leave the arithmetic exposed: 4096 x 4096 at 16 columns 7.30 -> 6.79 us)
+// and 4 above (14336 x 4096 at 16 columns: 15.2 us at 2 against 11.5).
+constexpr int64_t kMmqtSmallTiles = 512;
+int mmqt_sbw(int fmt, int S2, int64_t tiles) {
+    if ((S2 + 1) / 2 > 16 || fmt == RQ_FMT_Q6_K) return 4;
+    return fmt == RQ_FMT_Q4_K && tiles > kMmqtSmallTiles ? 4 : 2;
+}
 
 struct MmqPlan {
     int mp, g, sbw, ks, tr;  // mp = 16: the 16-column classes
@@ -713,7 +721,7 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
         sbw = ctx->mmq_sbw;
     else if (mp >= 8 && !dots)
         sbw = std::max(sbw, std::min(4, maxs));
-    if (mp == 16) sbw = mmqt_sbw(fmt, S2);
+    if (mp == 16) sbw = mmqt_sbw(fmt, S2, tiles);
     L.np = mmq_np(fmt, S2);
     if (L.np > 1) sbw = 4;  // the wide kernels: 16 k-parts of 4 per tile, in passes
     L.sbw = sbw;

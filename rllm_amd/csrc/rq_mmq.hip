@@ -877,7 +877,7 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
     u32 ksc[SBW][2];
     float kd[SBW];
     float cb4[SBW][2];
-    constexpr bool AMASK = FMT != RQ_FMT_Q4_0 && (G == 1 || (FMT == RQ_FMT_Q8_0 && G == 2 && SBW == 2 && !GLU));
+    constexpr bool AMASK = FMT != RQ_FMT_Q4_0 && (G == 1 || (G == 2 && SBW == 2 && !GLU));
     // AMASK: A register sets of blocks 0 and 1 of a window; a lane only ever
     // writes the one of its own block (g / 2), so the other stays zero.
     // Otherwise the B masks of MFMA h: the nibble (or byte) mask where the
