@@ -478,15 +478,18 @@ __device__ __forceinline__ void stage_write(const StageItem& si, XJ& x, int S) {
     }
 }
 
-// Staging by halves (the plain matvecs, stage_columns' HALVES): when a
+// Staging by halves (the one-column matvecs, mixed ones included:
+// stage_columns' HALVES): when a
 // workgroup's threads outnumber twice its blocks, thread h stages the 16-byte
 // half h % 2 of block item h / 2 (one code load and one scale load per thread,
 // against three loads for each of two items), the two halves' code sums meet
 // across the lane pair, and the even lane writes the block's per-block
 // values. Every lane of the wave must be active. (Q4_K 14336 x 4096, one
-// column: 6.947 -> 6.906 us. In the gated-FFN kernel the compiler then waited
-// for all weight loads before the staging barrier: 13.6 -> 14.2 us, so that
-// one keeps the item staging.)
+// column: 6.947 -> 6.906 us; the q/k/v launch of an 8B-shape layer, Q4_K and
+// Q6_K targets: 5.64 -> 5.27 us. In the gated-FFN kernel the compiler then
+// waited for all weight loads before the staging barrier: 13.6 -> 14.2 us;
+// with the staging path fixed at compile time it did not, but the launch
+// stayed as fast as with the item staging, so that one keeps the latter.)
 struct XHalf {
     StageItem si;
     int4 q;
@@ -870,7 +873,7 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const int8_t* xq = F32IN ? nullptr : sgpr_value(P.xq);  // first kernarg batch (as mvx_body)
     const u16* xd = F32IN ? nullptr : sgpr_value(P.xd);
     const float* xf = F32IN ? sgpr_value(P.xf) : nullptr;
-    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES>(xq, xd, xf, S, k,
+    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k,
                                                   [&] { load(has_tile ? t : T.w.T - 1, tl.slot); });
     if (!has_tile) return;
 
