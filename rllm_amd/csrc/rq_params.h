@@ -24,10 +24,12 @@
 //   Q8_0  C = 17  c0: the eight blocks' f16 d
 //                 c1+2j+h: block j's codes 16h .. 16h+15
 //   Q6_K  C = 13  c0: the 16 int8 sub-scales (GGUF bytes 192..207)
-//                 c1+j: sub-block j low nibbles, byte b = lo(q[b]) | lo(q[b+16]) << 4
-//                 c9+i: high 2-bit pairs of sub-blocks 2i, 2i+1, four dwords
-//                       H(2i,0) H(2i,1) H(2i+1,0) H(2i+1,1); H(j,h) holds
-//                       element 32j+16h+4c+e's two bits at bit 8e + 2c
+//                 c1+4w+i (w = 0..2, i = 0..3): with u = q XOR 32 for the
+//                       6-bit code q of an element, byte b holds in bits 7..2
+//                       the u of element 64w + 16i + b and in bits 1..0 bits
+//                       2w+1 .. 2w of the u of element 192 + 16i + b. Masked
+//                       with 0xFC a byte reads as the signed 4 (q - 32) of the
+//                       first; the three 2-bit pieces give the second's.
 //         tail plane: f16 d per slot, tail + (t * R * S + a) * 2
 //
 // Byte count per super-block equals GGUF's (144, 144, 272, 210): the repack
@@ -42,7 +44,8 @@
 #define RQ_FMT_Q6_K 3
 #define RQ_NUM_FMTS 4
 // Staging pseudo-format of launches that mix Q4_K and Q6_K targets (Q4_K_M
-// files keep attn_v and ffn_down in Q6_K): records carry both formats' sums.
+// files keep attn_v and ffn_down in Q6_K): records carry Q4_K's sums, which
+// Q6_K's dots do not need.
 #define RQ_FMT_MIX_K 8
 
 // Chunks of 16 bytes per super-block, by format.
