@@ -731,8 +731,9 @@ def main() -> int:
         log(f"8B-shape decode step (f32 inputs, quantized in each call): {f32['us']:.0f} us median "
             f"({f32['spread']['min']}-{f32['spread']['max']}), {f32['tok_s']:.1f} tok/s")
     if not args.no_decode and args.all_configs:
-        # The same step for a continuous batch of m tokens on int8-MFMA weights.
-        for m in (8, 32):
+        # The same step on int8-MFMA weights: one token (the cost of serving
+        # batch 1 from the MFMA layout alone) and continuous batches of m tokens.
+        for m in (1, 8, 32):
             b = bench_decode(torch, gpu, orc, 5, 1, m, "mfma")
             for how, bv in (("Q8_1 from the producers", b), ("f32 inputs", b["f32in"])):
                 log(f"8B-shape decode step, batch {m} (mfma, {how}): {bv['us']:.0f} us, {bv['tok_s']:.1f} tok/s")
