@@ -385,11 +385,13 @@ def test_mixed_q4k_q6k_launch(gpu, orc, family, k, m):
                               gpu.to_host(alone_q, m * n).view(np.uint32)), f"type {t} rows {n} (matvec_many)"
 
 
+@pytest.mark.parametrize("k", [1024, 5120, 14336])
 @pytest.mark.parametrize("tname", list(TYPES))
-def test_upload_roundtrip(gpuk, orc, tname):
-    """The repack moves bytes only: downloading it back gives the GGUF bytes."""
+def test_upload_roundtrip(gpuk, orc, tname, k):
+    """The repack moves bytes only: downloading it back gives the GGUF bytes
+    (tiles of 16, 2 and 1 rows: 4, 20 and 56 super-blocks per row)."""
     t = TYPES[tname]
-    n, k = 37, 1024
+    n = 37
     w = make_weight(orc, t, n, k, 91, "random")
     wg = upload(gpuk, t, w, n, k)
     assert wg.device_bytes >= w.nbytes
