@@ -426,11 +426,18 @@ rq_status matvec_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
         RqMvParams p;
         memset(&p, 0, sizeof p);
         int64_t waves = 0;
+        // A mixed launch puts its Q6_K targets first: their waves, with 13
+        // chunks against Q4_K's 9, start first. Each target keeps its own
+        // output, so the order changes no result.
+        int order[RQ_MV_TARGETS];
+        for (int i = 0, o = 0; o < 2; o++)
+            for (int j = 0; j < count; j++)
+                if ((ws[j]->fmt == RQ_FMT_Q6_K) == (o == 0)) order[i++] = j;
         for (int i = 0; i < count; i++) {
-            const rq_weight* w = ws[i];
+            const rq_weight* w = ws[order[i]];
             p.t[i].w = w->tiled;
             p.t[i].w.P = kp;
-            p.t[i].out = outs[i] + g0 * w->rows;
+            p.t[i].out = outs[order[i]] + g0 * w->rows;
             p.t[i].n = (int32_t)w->rows;
             p.t[i].wave_start = (int32_t)waves;
             waves += (int64_t)w->tiled.T * kp;
@@ -842,11 +849,18 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
         RqMmqParams p;
         memset(&p, 0, sizeof p);
         int64_t wgs = 0;
+        // Q6_K targets first, as in the dot4 launches (their workgroups carry
+        // more work); each target keeps its own output.
+        int order[RQ_MV_TARGETS];
+        for (int i = 0, o = 0; o < 2; o++)
+            for (int j = 0; j < count; j++)
+                if ((ws[j]->fmt == RQ_FMT_Q6_K) == (o == 0)) order[i++] = j;
         for (int i = 0; i < count; i++) {
-            const rq_weight* w = ws[i];
+            const rq_weight* w = ws[order[i]];
+            void* o = outs[order[i]];
             p.t[i].code = w->code;
             p.t[i].hdr = w->hdr;
-            p.t[i].out = dots ? (void*)((int32_t*)outs[i] + g0 * w->rows * nb) : (void*)((float*)outs[i] + g0 * w->rows);
+            p.t[i].out = dots ? (void*)((int32_t*)o + g0 * w->rows * nb) : (void*)((float*)o + g0 * w->rows);
             p.t[i].n = (int32_t)w->rows;
             p.t[i].tiles = w->tiles;
             p.t[i].wg_start = (int32_t)wgs;
