@@ -114,8 +114,10 @@ struct SB {
 // whole of its arithmetic followed the last of them; interleaved, each wave's
 // chunks arrive spread out and little of its work is left after its last one
 // (one column, Q4_K 14336 x 4096: 7.26 -> 7.16 us; 4096 x 4096: 3.98 ->
-// 3.83 us; Q6_K 4096 x 14336: 9.82 -> 9.64 us; Q8_0 gained nothing). Every
-// wave of the workgroup must make the call.
+// 3.83 us; Q6_K 4096 x 14336: 9.82 -> 9.64 us; Q8_0 gained nothing; with
+// Q6_K's codes as 4 (q - 32) bytes, barriers after 12, 4 or no chunks
+// instead of 8 were slower: 9.24 against 9.29 / 9.35 / 9.33 us). Every wave
+// of the workgroup must make the call.
 template <int FMT, bool WAVE_ORDER = false>
 __device__ __forceinline__ void load_sb(const RqTiled& w, int t, int a, SB<FMT>& o) {
     constexpr int C = Fmt<FMT>::C;
