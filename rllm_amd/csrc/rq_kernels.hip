@@ -979,23 +979,6 @@ RQ_MVX_ALL(q6_k, RQ_FMT_Q6_K)
 // are the ones a separate quantize of h gives). Needs R <= 32 (two or more
 // super-blocks per row) and n % 32 == 0.
 
-
-// Q8_1 of the 32 values held by lanes 0..31 (v) and 32..63 (another 32, or
-// zeros): every lane of the wave active; lane l < 32 gets its code, lane 0 of
-// each half the block's f16 d and s. Same rounding as rq_quantize_q8_1.
-__device__ __forceinline__ void q8_block32(float v, int& q, u16& d16, u16& s16) {
-    float amax = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    const float d = amax / 127.0f;
-    q8_codes<1>(&v, d, &q);
-    int sum = q;
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o);
-    d16 = f2h(d);
-    s16 = f2h_mul(d, (float)sum);
-}
-
 template <int FMT, int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void glu_body(const RqGluParams& P) {
     const int lane = threadIdx.x & 63;
@@ -1040,22 +1023,19 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
         w = wn;
     }
     __syncthreads();
-    // Epilogue: waves take the columns in turn; lanes 32..63 mirror 0..31.
+    // Epilogue: waves take the columns in turn; the column's 32 rows are one
+    // Q8_1 block, four rows to each of lanes 0..7 (lanes 8..63 mirror them),
+    // so amax and the code sum meet in three DPP steps (q8_emit4, the
+    // arithmetic of rq_quantize_q8_1) instead of ten cross-lane shuffles.
     for (int c = wave; c < NC && c < P.m; c += WAVES) {  // uniform per wave
-        const int r = lane & 31;
-        const float h = act_apply(P.act, gu[c * 32 + r]) * gu[(NC + c) * 32 + r];
-        const int64_t o = (int64_t)c * P.n + (int64_t)blk * 32 + r;
-        if (P.hf && lane < 32) P.hf[o] = h;
-        if (P.hq) {
-            int q;
-            u16 d16, s16;
-            q8_block32(lane < 32 ? h : 0.f, q, d16, s16);
-            if (lane < 32) P.hq[o] = (int8_t)q;
-            if (lane == 0) {
-                P.hd[o >> 5] = d16;
-                P.hs[o >> 5] = s16;
-            }
-        }
+        const int f4 = lane & 7;
+        float h[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            h[j] = act_apply(P.act, gu[c * 32 + 4 * f4 + j]) * gu[(NC + c) * 32 + 4 * f4 + j];
+        const int64_t o = (int64_t)c * P.n + (int64_t)blk * 32;  // the block's first row (n % 32 == 0)
+        if (P.hf && lane < 8) *(float4*)(P.hf + o + 4 * f4) = make_float4(h[0], h[1], h[2], h[3]);
+        if (P.hq) q8_emit4(h, (o >> 2) + f4, lane < 8, P.hq, P.hd, P.hs);
     }
 }
 
