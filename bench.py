@@ -620,6 +620,9 @@ def main() -> int:
     ap.add_argument("--all-configs", action="store_true",
                     help="also the sweeps (both families at 1-32 columns, Q6_K batches, shard shapes, batch decode)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the headline leg (its graph replays and nothing else: no floors, cold launch, "
+                         "traffic, configs, decode or CPU baseline), so that a kernel trace holds only its launches")
     ap.add_argument("--kernels", choices=["auto", "dot4", "mfma"], default="auto",
                     help="kernel family weights are laid out for (librq's RQ_KERNELS)")
     args = ap.parse_args()
@@ -631,6 +634,9 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+    if args.headline_only:
+        args.no_traffic = args.no_configs = args.no_decode = args.no_cpu = True
+        args.all_configs = False
     traffic = None if args.no_traffic else measure_traffic()
     if traffic:
         log(f"traffic: {traffic['bytes'] / 1e6:.2f} MB per launch: read {traffic['read']:.0f} B (DRAM "
@@ -649,20 +655,23 @@ def main() -> int:
     log(f"Q4_K {N}x{K} m=1 ({r['kernels']}): {r['us']:.3f} us/launch median over {args.steps} steps of "
         f"{r['launches_per_step']} launches (min {r['spread']['min']}, max {r['spread']['max']}), {r['gbs']:.0f} GB/s "
         f"({100 * r['gbs'] / HBM_PEAK_GBS:.1f}% of peak), {r['copies']} copies, check rel {r['check_rel']:.1e}")
-    floor = bench_floor(torch, gpu, T, N, K, args.steps, args.warmup)
+    floor = None if args.headline_only else bench_floor(torch, gpu, T, N, K, args.steps, args.warmup)
     if floor:
         log(f"read floor (same launch shape and bytes, no arithmetic): {floor['us']:.3f} us, "
             f"{alg_bytes(T, N, K, 1) / floor['us'] / 1e3:.0f} GB/s")
     # What bounds the decode step's smaller launches: the read floor of the
     # 4096 x 4096 shape (attn_output) and the fixed cost of a launch.
-    floor_small = bench_floor(torch, gpu, T, 4096, K, args.steps, args.warmup)
-    empty = bench_launch_floor(torch, gpu, N, args.steps, args.warmup)
+    floor_small = None if args.headline_only else bench_floor(torch, gpu, T, 4096, K, args.steps, args.warmup)
+    empty = None if args.headline_only else bench_launch_floor(torch, gpu, N, args.steps, args.warmup)
     if floor_small and empty:
         log(f"read floor of Q4_K 4096x4096: {floor_small['us']:.3f} us; empty launch (same grid as the headline): "
             f"{empty['us']:.3f} us")
 
-    cold_us = bench_cold(torch, gpu, orc, T, N, K)
-    log(f"cold (caches flushed, one eager launch): {cold_us:.2f} us, {alg_bytes(T, N, K, 1) / cold_us / 1e3:.0f} GB/s")
+    cold_us = None
+    if not args.headline_only:
+        cold_us = bench_cold(torch, gpu, orc, T, N, K)
+        log(f"cold (caches flushed, one eager launch): {cold_us:.2f} us, "
+            f"{alg_bytes(T, N, K, 1) / cold_us / 1e3:.0f} GB/s")
 
     configs = []
     if not args.no_configs:
@@ -781,7 +790,7 @@ def main() -> int:
                    "timing": "HIP events between graph replays on the replay stream; value at the median step"},
         "spread_us_per_launch": r["spread"],
         "pct_hbm_peak": round(100 * r["gbs"] / HBM_PEAK_GBS, 2),
-        "cold_us": round(cold_us, 2),
+        "cold_us": round(cold_us, 2) if cold_us else None,
         "decode_tok_s": round(dec["tok_s"], 1) if dec else None,
         "decode_step_us": round(dec["us"], 1) if dec else None,
         "decode_spread_us": dec["spread"] if dec else None,

@@ -194,7 +194,8 @@ rq_status rq_matmul_many(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m, 
                          float* const* outs, const int64_t* out_lens, int count);
 
 /* Most activation values (m * k) rq_matmul_many_noalloc takes: the capacity
- * of its fixed device scratch (2 MiB of codes + 2 x 64 KiB of f16 scales). */
+ * of its fixed device scratch (2 MiB of codes + 2 x 128 KiB of f16 scales, 2.25 MiB
+ * in all). */
 #define RQ_NOALLOC_MAX_VALUES (1 << 21)
 
 /* rq_matmul_many without any allocation. No counterpart in the reference: it

@@ -858,8 +858,9 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     }
 
 // Launches whose targets mix Q4_K and Q6_K weights of one width (q, k and v
-// of a Q4_K_M layer in one launch). The staged records carry both formats'
-// sums, each wave runs its own target's format, and the weights land in one
+// of a Q4_K_M layer in one launch). The staged records carry Q4_K's sums
+// (Q6_K's dots, over its XOR-32 codes, need none), each wave runs its own
+// target's format, and the weights land in one
 // register block sized for Q6_K (Q4_K fills the first 9 chunks), so the two
 // formats share registers instead of adding up.
 template <int NC, bool F32IN, int WAVES>

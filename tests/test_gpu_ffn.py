@@ -207,7 +207,7 @@ def test_gated_ffn_q8_1_input(gpuk, orc, tname, m):
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
-@pytest.mark.parametrize("d", [5120, 8192, 14336, 20480])
+@pytest.mark.parametrize("d", [5120, 8192, 14336, 20480, 32768])
 @pytest.mark.parametrize("m", [1, 3, 8, 12])
 def test_gated_ffn_wide_inputs(gpuk, orc, tname, d, m):
     """Inputs wider than 16 super-blocks: the fused MFMA front half walks the

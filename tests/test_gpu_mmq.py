@@ -63,6 +63,14 @@ def test_mmq_widths(mfma, orc, tname, k, m):
     _run(mfma, orc, MMQ_TYPES[tname], 33, k, m, 17 * k + m, kind="normal")
 
 
+@pytest.mark.parametrize("tname", list(MMQ_TYPES))
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_mmq_widest_rows(mfma, orc, tname, m):
+    """k = 65536, the widest row the planner accepts (4 passes of the wide
+    kernels; one column's staging is the largest that fits LDS)."""
+    _run(mfma, orc, MMQ_TYPES[tname], 17, 65536, m, 65536 + m, kind="normal")
+
+
 @pytest.mark.parametrize("tname", ["Q4_0", "Q8_0"])
 @pytest.mark.parametrize("k", [32, 32 * 65, 32 * 17])
 def test_mmq_partial_super_blocks(mfma, orc, tname, k):

@@ -60,3 +60,66 @@ def test_noalloc_capacity(gpu, orc):
     assert torch.equal(out[:m * n].view(torch.int32), want.view(torch.int32))
     with pytest.raises(ShapeError, match="fixed scratch"):
         gpu.matmul_many_noalloc(x, [w], [out], m + 1)
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+@pytest.mark.parametrize("family", ["dot4", "mfma"])
+def test_noalloc_under_capture_on_a_fresh_context(orc, family):
+    """What the entry point is for: on a context that has never allocated
+    scratch (no rq_reserve, no earlier m >= 2 call), rq_matmul_many_noalloc
+    at m >= 2 records into a HIP graph, where rq_matmul_many's scratch growth
+    is refused, and every replay equals an eager call bit for bit. Device
+    memory that the library could have taken does not change."""
+    from rllm_amd.backend import HipBackend
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    fresh = HipBackend(0)
+    try:
+        fresh.set_kernels(family)
+        k, m = 4096, 6
+        spec = [(12, 128), (12, 64), (14, 64)]
+        ws = [upload(fresh, t, make_weight(orc, t, n, k, 700 + i, "normal"), n, k) for i, (t, n) in enumerate(spec)]
+        x = fresh.from_host(orc.normal(710, m * k))
+        g_outs = [fresh.alloc(m * n) for _, n in spec]
+        # rq_matmul_many would have to grow the context's scratch: refused.
+        with pytest.raises(ShapeError, match="rq_reserve"):
+            _capture(fresh, lambda: fresh.matmul_many(x, ws, g_outs, m))
+        torch.cuda.synchronize()
+        free0, _ = torch.cuda.mem_get_info(fresh.device)
+        g = _capture(fresh, lambda: fresh.matmul_many_noalloc(x, ws, g_outs, m))
+        for rep in range(3):
+            x.copy_(torch.from_numpy(orc.normal(720 + rep, m * k)).to(fresh.device))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = [o.clone() for o in g_outs]
+            want = _run(fresh, fresh.matmul_many_noalloc, x, ws, m)
+            for a, b in zip(got, want):
+                assert np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32)), f"replay {rep} differs"
+        free1, _ = torch.cuda.mem_get_info(fresh.device)
+        # torch's own graph pool may take a few MiB; the library's scratch for
+        # this call (m * k codes + scales) would be in addition, and is not.
+        assert free0 - free1 < (64 << 20), f"device memory dropped by {(free0 - free1) >> 20} MiB"
+        # and the last replay equals rq_matmul_many (which now grows its scratch)
+        want = _run(fresh, fresh.matmul_many, x, ws, m)
+        for a, b in zip(got, want):
+            assert np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32)), "noalloc != matmul_many"
+        del g
+    finally:
+        fresh.synchronize()
+        fresh.close()
+
+
+def _capture(gpu, fn):
+    s = torch.cuda.Stream(gpu.device)
+    main = torch.cuda.current_stream(gpu.device)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    gpu.set_stream(s)
+    try:
+        with torch.cuda.graph(g, stream=s):
+            fn()
+    finally:
+        gpu.set_stream(main)
+    return g
