@@ -957,9 +957,11 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
     for (;;) {
         MmqPlan L;
         int h_off;
-        plan((int)((m + ngroups - 1) / ngroups), L, h_off);
+        const int nc = (int)((m + ngroups - 1) / ngroups);
+        plan(nc, L, h_off);
         if (L.lds <= ctx->lds_wide) break;
-        if (m / ngroups <= 1) return fail(RQ_ERR_SHAPE, "glu: %lld columns too wide to stage", (long long)k);
+        // Fewer columns per launch until one column alone does not fit.
+        if (nc == 1) return fail(RQ_ERR_SHAPE, "glu: %lld columns too wide to stage", (long long)k);
         ngroups++;
     }
     for (int64_t gi = 0, g0 = 0; gi < ngroups; gi++) {
