@@ -2,7 +2,7 @@
 
 1. hipcc --genco compiles each kernel source (csrc/rq_kernels.hip: the Q8_1
    pass and the dot4 matvecs; csrc/rq_mmq.hip: the int8-MFMA matvecs) into
-   one gfx950 code object.
+   one gfx950 code object each.
 2. An assembler stub (.incbin) embeds the code objects in the library.
 3. hipcc compiles csrc/rq_static.hip (the fixed device scratch of
    rq_matmul_many_noalloc) as an ordinary host + device object.
@@ -11,6 +11,9 @@
 
 The result, rllm_amd/lib/librq.so, is self-contained: rq_open() loads the
 embedded code objects with hipModuleLoadData; nothing is compiled at run time.
+The same steps with -DRQ_TIMELINE build rllm_amd/lib/librq_tl.so, whose
+kernels also record per-wave timestamps (include/rq_timeline.h; only
+bench.py --timeline loads it).
 
 Usage: python -m rllm_amd.build   (or rllm_amd.build.build()).
 """
@@ -28,6 +31,8 @@ LIB = os.path.join(LIBDIR, "librq.so")
 # bench.py's roofline reference (a read-only kernel of the matvec's launch
 # shape); not part of librq.so.
 FLOOR_LIB = os.path.join(LIBDIR, "librq_floor.so")
+# librq.so with per-wave timestamps (bench.py --timeline).
+TIMELINE_LIB = os.path.join(LIBDIR, "librq_tl.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 # Kernel sources, one code object each (embedded as <name>_blob).
@@ -65,32 +70,11 @@ def _run_all(cmds: list[list[str]]) -> None:
         _check(c, rc, out)
 
 
-def build(verbose: bool = False, csrc: str = CSRC, libdir: str = LIBDIR, builddir: str = BUILD,
-          floor: bool = True) -> str:
-    """Compile everything; returns the library path. `csrc`, `libdir` and
-    `builddir` default to the package's own (a build of another source tree
-    goes elsewhere); the kernel sources compile in parallel."""
-    os.makedirs(builddir, exist_ok=True)
-    os.makedirs(libdir, exist_ok=True)
-    hipcc = os.path.join(ROCM, "bin", "hipcc")
-    lib = os.path.join(libdir, "librq.so")
-    blob = os.path.join(builddir, "rq_blob.S")
-    static_obj = os.path.join(builddir, "rq_static.o")
-    jobs = [[hipcc, "--genco", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, f"{name}.hip"), "-o",
-             os.path.join(builddir, f"{name}.hsaco")] for name in KERNEL_SOURCES]
-    # The fixed scratch of rq_matmul_many_noalloc: a device array in a HIP
-    # translation unit of its own (host + gfx950 device code, registered with
-    # the HIP runtime when the library loads).
-    jobs.append([hipcc, "-c", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_static.hip"), "-o", static_obj])
-    floor_lib = os.path.join(libdir, "librq_floor.so")
-    if floor:
-        # bench.py's read-floor probe (rq_floor.hip), a library of its own.
-        jobs.append([hipcc, "-shared", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_floor.hip"), "-o",
-                     floor_lib + ".tmp"])
-    _run_all(jobs)
+def _blob_stub(builddir: str, tag: str) -> str:
+    """The assembler stub embedding the code objects <name><tag>.hsaco."""
     stub = []
     for name in KERNEL_SOURCES:
-        hsaco = os.path.join(builddir, f"{name}.hsaco")
+        hsaco = os.path.join(builddir, f"{name}{tag}.hsaco")
         stub += [
             "    .section .rodata\n",
             "    .balign 4096\n",
@@ -102,17 +86,55 @@ def build(verbose: bool = False, csrc: str = CSRC, libdir: str = LIBDIR, builddi
             f"    .size {name}_blob, . - {name}_blob\n",
         ]
     stub.append('    .section .note.GNU-stack,"",@progbits\n')
+    blob = os.path.join(builddir, f"rq_blob{tag}.S")
     with open(blob, "w") as f:
         f.write("".join(stub))
-    tmp = lib + ".tmp"
-    _run([
-        "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra",
+    return blob
+
+
+def _link(csrc: str, blob: str, static_obj: str, out: str, defines: list[str]) -> list[str]:
+    return [
+        "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra", *defines,
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{csrc}",
         os.path.join(csrc, "rq_host.cpp"), os.path.join(csrc, "rq_gguf.cpp"), blob, static_obj,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
-        "-o", tmp,
-    ])
+        "-o", out,
+    ]
+
+
+def build(verbose: bool = False, csrc: str = CSRC, libdir: str = LIBDIR, builddir: str = BUILD,
+          floor: bool = True, timeline: bool = True) -> str:
+    """Compile everything; returns the library path. `csrc`, `libdir` and
+    `builddir` default to the package's own (a build of another source tree
+    goes elsewhere); the kernel sources compile in parallel."""
+    os.makedirs(builddir, exist_ok=True)
+    os.makedirs(libdir, exist_ok=True)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    lib = os.path.join(libdir, "librq.so")
+    static_obj = os.path.join(builddir, "rq_static.o")
+    tags = ["", "_tl"] if timeline else [""]
+    jobs = [[hipcc, "--genco", *HIPCC_FLAGS, *(["-DRQ_TIMELINE"] if tag else []), f"-I{csrc}",
+             os.path.join(csrc, f"{name}.hip"), "-o", os.path.join(builddir, f"{name}{tag}.hsaco")]
+            for tag in tags for name in KERNEL_SOURCES]
+    # The fixed scratch of rq_matmul_many_noalloc: a device array in a HIP
+    # translation unit of its own (host + gfx950 device code, registered with
+    # the HIP runtime when the library loads).
+    jobs.append([hipcc, "-c", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_static.hip"), "-o", static_obj])
+    floor_lib = os.path.join(libdir, "librq_floor.so")
+    if floor:
+        # bench.py's read-floor probe (rq_floor.hip), a library of its own.
+        jobs.append([hipcc, "-shared", "-fPIC", *HIPCC_FLAGS, f"-I{csrc}", os.path.join(csrc, "rq_floor.hip"), "-o",
+                     floor_lib + ".tmp"])
+    _run_all(jobs)
+    tmp = lib + ".tmp"
+    links = [_link(csrc, _blob_stub(builddir, ""), static_obj, tmp, [])]
+    tl_lib = os.path.join(libdir, "librq_tl.so")
+    if timeline:
+        links.append(_link(csrc, _blob_stub(builddir, "_tl"), static_obj, tl_lib + ".tmp", ["-DRQ_TIMELINE"]))
+    _run_all(links)
     os.replace(tmp, lib)
+    if timeline:
+        os.replace(tl_lib + ".tmp", tl_lib)
     if floor:
         os.replace(floor_lib + ".tmp", floor_lib)
     if verbose:

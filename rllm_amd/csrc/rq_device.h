@@ -73,6 +73,39 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 // v_dot4_i32_i8: c + sum of the four signed byte products.
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// ---------------------------------------------------------------------------
+// Per-wave timeline, compiled only into librq_tl.so (-DRQ_TIMELINE; bench.py
+// --timeline): a kernel keeps up to RQ_TL_MARKS stamps of the 100 MHz
+// real-time counter in scalar registers (RqTl) and, at its end, lane 0 of
+// each wave stores them with vector stores into this code object's rq_tl
+// array at slot blockIdx.x * (waves per workgroup) + wave; each launch
+// overwrites its own slots. Stamps stored mid-kernel would not do: the
+// in-order vector-memory waits would then also wait for their writes. In the
+// library built without RQ_TIMELINE the marks compile to nothing.
+#define RQ_TL_MARKS 8
+#define RQ_TL_SLOTS 32768
+struct RqTl {
+    u64 t[RQ_TL_MARKS];
+};
+#ifdef RQ_TIMELINE
+__device__ u64 rq_tl[RQ_TL_SLOTS * RQ_TL_MARKS];
+__device__ __forceinline__ void tl_mark(RqTl& tl, int i) {
+    __builtin_amdgcn_sched_barrier(0);
+    tl.t[i] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void tl_store(const RqTl& tl) {
+    const int waves = (int)(blockDim.x >> 6), wave = (int)(threadIdx.x >> 6);
+    const int slot = (int)blockIdx.x * waves + wave;
+    if ((threadIdx.x & 63) == 0 && slot < RQ_TL_SLOTS)
+#pragma unroll
+        for (int i = 0; i < RQ_TL_MARKS; i++) rq_tl[(int64_t)slot * RQ_TL_MARKS + i] = tl.t[i];
+}
+#else
+__device__ __forceinline__ void tl_mark(RqTl&, int) {}
+__device__ __forceinline__ void tl_store(const RqTl&) {}
+#endif
+
 // Streaming 16-byte load of global memory: weights are read once, so the
 // nontemporal hint keeps them from displacing reusable lines (activations) in
 // the caches.

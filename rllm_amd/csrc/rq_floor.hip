@@ -13,6 +13,8 @@
 // rq_floor_empty launches the same grid with no work at all: the fixed cost
 // of one dependent launch in a replayed graph.
 
+#include <string.h>
+
 #include "rq_device.h"
 
 template <int C>
@@ -55,6 +57,165 @@ extern "C" int rq_floor_read(const void* base, int64_t tiles, int chunks, int la
     case 17: hipLaunchKernelGGL(rq_floor_read_k<17>, grid, block, 0, s, b, tiles, lanes_per_row, (u32*)out, rows); break;
     default: return (int)hipErrorInvalidValue;
     }
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The general form, for every launch of the decode step: up to three
+// targets (the mixed q/k/v launch), tiles of R rows x S super-blocks as the
+// dot4 layout stores them (R = 1 for rows of more than 32 super-blocks, as
+// ffn_down's 56), the Q6_K scale plane (2 B per slot), and `pair` = 1 for
+// the gated FFN's workgroups, whose wave w reads tile w of both gate and up.
+// Lane to slot mapping, padding lanes and the row reduction are the matvec's
+// (tile_lane, group_sum); the reads are its loads, with no arithmetic.
+struct RqFloorTarget {
+    const u8* base;  // chunk plane
+    const u8* tail;  // Q6_K f16 d per slot, or null
+    int64_t tiles;
+    int32_t chunks, R, S, pad;
+    u32* out;        // one word per row
+    int64_t rows;
+    int64_t wave0;   // first wave of the target (pair: 0 for both)
+};
+struct RqFloorParams {
+    RqFloorTarget t[3];
+    int32_t count;
+    int32_t pair;
+};
+
+// One tile's loads (C chunks, unrolled and unguarded as the matvec issues
+// them, then the scale-plane word), folded with XOR.
+template <int C>
+__device__ __forceinline__ int floor_tile_c(const RqFloorTarget& T, int64_t tile, int lane, int& row) {
+    int col;
+    bool real;
+    if (T.R > 1) {
+        const int sh = 6 - __builtin_ctz(T.R);
+        row = lane >> sh;
+        col = lane & ((1 << sh) - 1);
+        real = col < T.S;
+    } else {
+        row = 0;
+        col = lane;
+        real = lane < T.S;
+    }
+    const int64_t slots = (int64_t)T.R * T.S;
+    const int64_t slot = row * T.S + (real ? col : 0);
+    const u8* p = T.base + (tile * C * slots + slot) * 16;
+    int4 v[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) v[c] = ld16_nt(p + c * slots * 16);
+    int x = T.tail ? (int)*(const u16*)(T.tail + (tile * slots + slot) * 2) : 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) x ^= v[c].x ^ v[c].y ^ v[c].z ^ v[c].w;
+    return x;
+}
+
+// The target's chunk count picks the path (wave-uniform).
+__device__ __forceinline__ int floor_tile(const RqFloorTarget& T, int64_t tile, int lane, int& row) {
+    if (T.chunks == 9) return floor_tile_c<9>(T, tile, lane, row);
+    if (T.chunks == 13) return floor_tile_c<13>(T, tile, lane, row);
+    return floor_tile_c<17>(T, tile, lane, row);
+}
+
+__device__ __forceinline__ void floor_store(const RqFloorTarget& T, int64_t tile, int lane, int row, int x) {
+    const int g = T.R > 1 ? 64 >> __builtin_ctz(T.R) : 64;
+    if (g >= 2) x ^= dpp_i<DPP_QUAD_1032>(x);
+    if (g >= 4) x ^= dpp_i<DPP_QUAD_2301>(x);
+    if (g >= 8) x ^= dpp_i<DPP_ROW_HALF_MIRROR>(x);
+    if (g >= 16) x ^= dpp_i<DPP_ROW_MIRROR>(x);
+    if (g == 32) x ^= dpp_i<DPP_ROW_BCAST15, 0xA>(x);
+    if (g == 64)
+        x = (__builtin_amdgcn_readlane(x, 0) ^ __builtin_amdgcn_readlane(x, 16)) ^
+            (__builtin_amdgcn_readlane(x, 32) ^ __builtin_amdgcn_readlane(x, 48));
+    const bool leader = g == 32 ? (lane & 31) == 16 : (g == 64 ? lane == 0 : (lane & (g - 1)) == 0);
+    const int64_t r = tile * T.R + row;
+    if (leader && row < T.R && r < T.rows) T.out[r] = (u32)x;
+}
+
+// Target ti by value (the matvec kernels' pick_target): a reference indexed
+// by the runtime target number would reload its fields with dependent
+// kernarg loads ahead of the first weight load.
+__device__ __forceinline__ RqFloorTarget floor_pick(const RqFloorParams& P, int ti) {
+    RqFloorTarget r;
+#define RQ_FPICK(f)                                                                              \
+    {                                                                                            \
+        const auto a = sgpr_value(P.t[0].f), b = sgpr_value(P.t[1].f), c = sgpr_value(P.t[2].f); \
+        r.f = ti == 0 ? a : (ti == 1 ? b : c);                                                   \
+    }
+    RQ_FPICK(base)
+    RQ_FPICK(tail)
+    RQ_FPICK(tiles)
+    RQ_FPICK(chunks)
+    RQ_FPICK(R)
+    RQ_FPICK(S)
+    RQ_FPICK(out)
+    RQ_FPICK(rows)
+    RQ_FPICK(wave0)
+#undef RQ_FPICK
+    r.pad = 0;
+    return r;
+}
+
+template <int THREADS, bool PAIR>
+__global__ __launch_bounds__(THREADS) void rq_floor_many_k(RqFloorParams P) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (PAIR) {
+        if (gw >= P.t[0].tiles) return;  // wave-uniform
+        int r0, r1;
+        const int x0 = floor_tile(P.t[0], gw, lane, r0);
+        const int x1 = floor_tile(P.t[1], gw, lane, r1);
+        floor_store(P.t[0], gw, lane, r0, x0);
+        floor_store(P.t[1], gw, lane, r1, x1);
+        return;
+    }
+    int ti = 0;
+    if (P.count > 1 && gw >= P.t[1].wave0) ti = 1;
+    if (P.count > 2 && gw >= P.t[2].wave0) ti = 2;
+    const RqFloorTarget T = floor_pick(P, ti);
+    const int64_t tile = gw - T.wave0;
+    if (tile >= T.tiles) return;  // wave-uniform
+    int row;
+    const int x = floor_tile(T, tile, lane, row);
+    floor_store(T, tile, lane, row, x);
+}
+
+// Launches the general read floor: `count` targets one after the other in
+// the grid (or, with pair, two targets of equal tile counts side by side in
+// each wave), `threads` per workgroup (256, 512 or 1024). Returns a
+// hipError_t.
+extern "C" int rq_floor_read_many(const void* targets, int count, int pair, int threads, void* stream) {
+    if (!targets || count < 1 || count > 3 || (pair && (count != 2 || threads != 512)) ||
+        (threads != 256 && threads != 512 && threads != 1024))
+        return (int)hipErrorInvalidValue;
+    RqFloorParams P;
+    memset(&P, 0, sizeof P);
+    memcpy(P.t, targets, sizeof(RqFloorTarget) * count);
+    int64_t waves = 0;
+    for (int i = 0; i < count; i++) {
+        RqFloorTarget& T = P.t[i];
+        if (!T.base || !T.out || T.tiles <= 0 || T.rows <= 0 || T.R < 1 || T.R > 64 || (T.R & (T.R - 1)) ||
+            T.S < 1 || T.S > 64 || (T.R > 1 && T.S > 64 / T.R) || T.rows > T.tiles * T.R ||
+            (T.chunks != 9 && T.chunks != 13 && T.chunks != 17) || ((uintptr_t)T.base & 15))
+            return (int)hipErrorInvalidValue;
+        T.wave0 = pair ? 0 : waves;
+        waves = pair ? T.tiles : waves + T.tiles;
+    }
+    if (pair && P.t[0].tiles != P.t[1].tiles) return (int)hipErrorInvalidValue;
+    P.count = count;
+    P.pair = pair;
+    const int wpg = threads / 64;
+    const dim3 grid((unsigned)((waves + wpg - 1) / wpg)), block(threads);
+    hipStream_t s = (hipStream_t)stream;
+    if (pair)
+        hipLaunchKernelGGL((rq_floor_many_k<512, true>), grid, block, 0, s, P);
+    else if (threads == 256)
+        hipLaunchKernelGGL((rq_floor_many_k<256, false>), grid, block, 0, s, P);
+    else if (threads == 512)
+        hipLaunchKernelGGL((rq_floor_many_k<512, false>), grid, block, 0, s, P);
+    else
+        hipLaunchKernelGGL((rq_floor_many_k<1024, false>), grid, block, 0, s, P);
     return (int)hipGetLastError();
 }
 

@@ -1266,6 +1266,26 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     return RQ_OK;
 }
 
+#ifdef RQ_TIMELINE
+#include "../../include/rq_timeline.h"
+// The per-wave stamps of code object `which` (librq_tl.so only).
+extern "C" rq_status rq_timeline_read(rq_ctx* ctx, int which, void* host, int64_t bytes) {
+    if (!ctx || !host || bytes < 0) return fail(RQ_ERR_INVALID, "rq_timeline_read: null or negative argument");
+    if (which < 0 || which > 1) return fail(RQ_ERR_INVALID, "rq_timeline_read: code object %d (0 or 1)", which);
+    rq_status st = bind(ctx);
+    if (st != RQ_OK) return st;
+    hipModule_t mod = which == 0 ? ctx->mod : ctx->mmq_mod;
+    hipDeviceptr_t p = nullptr;
+    size_t size = 0;
+    hipError_t e = hipModuleGetGlobal(&p, &size, mod, "rq_tl");
+    if (e != hipSuccess) return hip_fail("hipModuleGetGlobal(rq_tl)", e);
+    if ((size_t)bytes > size) return fail(RQ_ERR_SHAPE, "rq_timeline_read: %lld bytes of %zu", (long long)bytes, size);
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail("hipStreamSynchronize", e);
+    if ((e = hipMemcpyDtoH(host, p, (size_t)bytes)) != hipSuccess) return hip_fail("hipMemcpyDtoH", e);
+    return RQ_OK;
+}
+#endif
+
 extern "C" rq_status rq_set_kernels(rq_ctx* ctx, int family) {
     if (!ctx) return fail(RQ_ERR_INVALID, "rq_set_kernels: null context");
     if (family != RQ_KERNELS_AUTO && family != RQ_KERNELS_DOT4 && family != RQ_KERNELS_MFMA && family != RQ_KERNELS_BOTH)

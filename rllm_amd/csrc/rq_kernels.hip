@@ -758,6 +758,10 @@ __device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
 // more than 64 super-blocks); without it, w.P is ignored.
 template <int FMT, int NC, bool F32IN, int WAVES, bool KP = false>
 __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
+    // Timeline marks (librq_tl.so only): 0 start, 1 weight loads issued,
+    // 2 staging done, 3 arithmetic done, 4 row sums stored.
+    RqTl tlm;
+    tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
     const int gwave = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // All targets of one launch share k, so the staged columns serve every wave.
@@ -793,7 +797,11 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
     constexpr bool ORDER = NC == 1 && !KP && FMT != RQ_FMT_Q8_0;
-    stage_columns<FMT, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] { load_sb<FMT, ORDER>(T.w, tc, tl.slot, w); });
+    stage_columns<FMT, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] {
+        load_sb<FMT, ORDER>(T.w, tc, tl.slot, w);
+        tl_mark(tlm, 1);
+    });
+    tl_mark(tlm, 2);
     if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
 
     float acc[NC];
@@ -808,6 +816,7 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
         load_sb<FMT>(T.w, tc, active ? a : 0, w2);
         slot_dot<FMT, NC>(w2, S, active ? a : 0, active, acc);
     }
+    tl_mark(tlm, 3);
     // Row sums: stored, or with k-parts left in LDS (wave w of the workgroup
     // at part_lds[w][c], after the staged records) for the tile's part-0
     // wave, which adds its kp waves' sums in part order and stores.
@@ -822,7 +831,11 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
             part_lds[wv * NC + c] = v;
         }
     }
-    if (kp == 1) return;
+    if (kp == 1) {
+        tl_mark(tlm, 4);
+        tl_store(tlm);
+        return;
+    }
     __syncthreads();
     if (part == 0 && dst.store) {
 #pragma unroll
@@ -865,6 +878,10 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
 // formats share registers instead of adding up.
 template <int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
+    // Timeline marks (librq_tl.so only), as mvx_body's: 0 start, 1 weight
+    // loads issued, 2 staging done, 3 arithmetic done, 4 row sums stored.
+    RqTl tlm;
+    tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
     const int gwave = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int S = P.t[0].w.S, k = P.t[0].w.k;
@@ -913,8 +930,11 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const int8_t* xq = F32IN ? nullptr : sgpr_value(P.xq);  // first kernarg batch (as mvx_body)
     const u16* xd = F32IN ? nullptr : sgpr_value(P.xd);
     const float* xf = F32IN ? sgpr_value(P.xf) : nullptr;
-    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k,
-                                                  [&] { load(has_tile ? t : T.w.T - 1, tl.slot); });
+    stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] {
+        load(has_tile ? t : T.w.T - 1, tl.slot);
+        tl_mark(tlm, 1);
+    });
+    tl_mark(tlm, 2);
     if (!has_tile) return;
 
     float acc[NC];
@@ -926,8 +946,11 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
         load(t, active ? a : 0);
         dot(active ? a : 0, active, acc);
     }
+    tl_mark(tlm, 3);
 #pragma unroll
     for (int c = 0; c < NC; c++) tile_store(dst, T.n, acc[c], c);
+    tl_mark(tlm, 4);
+    tl_store(tlm);
 }
 
 #define RQ_MVXM(NC)                                                                                                   \
@@ -982,6 +1005,11 @@ RQ_MVX_ALL(q6_k, RQ_FMT_Q6_K)
 
 template <int FMT, int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void glu_body(const RqGluParams& P) {
+    // Timeline marks (librq_tl.so only): 0 start, 1 first tile's loads
+    // issued, 2 staging done, 3 the wave's last tile's arithmetic done,
+    // 4 the block's g and u in LDS, 5 h and its Q8_1 stored.
+    RqTl tlm;
+    tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int S = P.gate.S, R = P.gate.R, k = P.gate.k;
@@ -995,8 +1023,11 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
     const int q0 = wave < 2 * NT ? wave : 0;
 
     SB<FMT> w;
-    stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k,
-                                         [&] { load_sb<FMT>(tile_w(q0), tile_t(q0), tl.slot, w); });
+    stage_columns<FMT, NC, F32IN, WAVES>(P.xq, P.xd, P.xf, S, k, [&] {
+        load_sb<FMT>(tile_w(q0), tile_t(q0), tl.slot, w);
+        tl_mark(tlm, 1);
+    });
+    tl_mark(tlm, 2);
     // g and u of the block, per column: floats after the staged records.
     float* gu = (float*)(rq_lds + NC * S * RQ_LDS_REC);
     for (int q = wave; q < 2 * NT; q += WAVES) {  // uniform per wave
@@ -1022,8 +1053,10 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
             if (group_leader(lane, g) && rt < R) gu[((q < NT ? 0 : NC) + c) * 32 + row] = v;
         }
         w = wn;
+        tl_mark(tlm, 3);
     }
     __syncthreads();
+    tl_mark(tlm, 4);
     // Epilogue: waves take the columns in turn; the column's 32 rows are one
     // Q8_1 block, four rows to each of lanes 0..7 (lanes 8..63 mirror them),
     // so amax and the code sum meet in three DPP steps (q8_emit4, the
@@ -1038,6 +1071,8 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
         if (P.hf && lane < 8) *(float4*)(P.hf + o + 4 * f4) = make_float4(h[0], h[1], h[2], h[3]);
         if (P.hq) q8_emit4(h, (o >> 2) + f4, lane < 8, P.hq, P.hd, P.hs);
     }
+    tl_mark(tlm, 5);
+    tl_store(tlm);
 }
 
 // Workgroup width: each wave holds two tiles' weights (the one it computes

@@ -818,6 +818,11 @@ __device__ __forceinline__ void mmqt_reduce_glu(const RqMmqParams& P, const RqMm
 
 template <int FMT, int SBW, int G, bool GLU>
 __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
+    // Timeline marks (librq_tl.so only): 0 start, 1 first loads issued, then
+    // per column group gi < 2: 2 + 3 gi staged, 3 + 3 gi products done,
+    // 4 + 3 gi sums stored.
+    RqTl tlm;
+    tl_mark(tlm, 0);
     constexpr bool NIB = MF<FMT>::NIB;
     constexpr int LPS = NIB ? 2 : 4;  // code loads per super-block
     constexpr int NLD = LPS * SBW;
@@ -870,6 +875,7 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
 #pragma unroll
     for (int i = 0; i < PRE; i++) load_sb(i);
     __builtin_amdgcn_sched_barrier(0);
+    tl_mark(tlm, 1);
 
     // Per super-block, decoded at group 0 and kept for the later groups:
     // Q4_K the two scale words and d (q4k_decode); the correction operand c
@@ -900,6 +906,7 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
     mmqt_stage<FMT>(P, gi, x0, x1);
+    if (gi < 2) tl_mark(tlm, 2 + 3 * gi);
     if (gi + 1 < G) mmqt_prefetch(P, gi + 1, x0, x1);
     v4f y = {0.f, 0.f, 0.f, 0.f};
 
@@ -996,6 +1003,7 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
     // The group's k-part sums meet in a fixed order: stored, or (GLU) h.
     // (The fused FFN's partial sums sit over the staged codes: every wave is
     // done reading them first.)
+    if (gi < 2) tl_mark(tlm, 3 + 3 * gi);
     if (GLU) __syncthreads();
     *(v4f*)(part + (wave * 64 + lane) * 4) = y;
     __syncthreads();
@@ -1003,7 +1011,9 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
         mmqt_reduce(P, T, gi, part);
     else
         mmqt_reduce_glu(P, T, gi, part);
+    if (gi < 2) tl_mark(tlm, 4 + 3 * gi);
     }  // column groups
+    tl_store(tlm);
 }
 
 // ---------------------------------------------------------------------------

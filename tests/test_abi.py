@@ -113,3 +113,20 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "librq.so"))
     with pytest.raises(RllmError, match="not built"):
         _lib.lib()
+
+
+def test_timeline_library_exports_the_abi_and_its_reader():
+    """librq_tl.so (the -DRQ_TIMELINE build bench.py --timeline loads)
+    exports include/rq.h's symbols plus include/rq_timeline.h's, nothing
+    else."""
+    import subprocess
+
+    from rllm_amd import build as rq_build
+
+    if not os.path.exists(rq_build.TIMELINE_LIB):
+        pytest.skip("librq_tl.so not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", rq_build.TIMELINE_LIB], capture_output=True, text=True,
+                         check=True).stdout
+    funcs = sorted(l.split()[-1] for l in out.splitlines() if " T " in l)
+    want = sorted(_lib.declared_symbols() + _lib.declared_symbols(os.path.join(ROOT, "include", "rq_timeline.h")))
+    assert funcs == want
