@@ -605,7 +605,7 @@ def traffic_child(argv) -> int:
 
 
 # Marks of the instrumented kernels (include/rq_timeline.h).
-MARKS_MV = ["start", "loads issued", "staged", "arithmetic done", "stored"]
+MARKS_MV = ["start", "loads issued", "staged", "arithmetic done", "stored", "preamble done"]
 MARKS_MMQT = ["start", "first loads issued", "group 0 staged", "group 0 products", "group 0 stored", "group 1 staged",
               "group 1 products", "group 1 stored"]
 MARKS_GLU = ["start", "loads issued", "staged", "last tile's arithmetic", "g and u in LDS", "stored"]
@@ -672,6 +672,7 @@ def timeline(argv) -> int:
     _, g = time_graph(torch, gpu, launch, chunk, 1, 2)
     buf = np.zeros(slots * marks, dtype=np.uint64)
     per_mark, spans, which = [], [], None
+    last_mark = {False: -1, True: MARKS_MV.index("stored")}  # the span ends at the final store
     for _ in range(replays):
         g.replay()
         torch.cuda.synchronize()
@@ -686,7 +687,7 @@ def timeline(argv) -> int:
             raise RuntimeError("no instrumented kernel ran (the timeline covers rq_mvx*, rq_glu*, rq_mmq_*_16x*)")
         names = MARKS_GLU if kind == "glu" else (MARKS_MV if which == 0 else MARKS_MMQT)
         rel = (live[:, :len(names)].astype(np.int64) - int(live[:, 0].min())) * 0.01  # 100 MHz ticks -> us
-        spans.append(float(rel[:, -1].max()))
+        spans.append(float(rel[:, last_mark[names is MARKS_MV]].max()))
         per_mark.append([[float(np.percentile(rel[:, i], q)) for q in (10, 50, 90, 100)] for i in range(len(names))])
     pm = np.median(np.asarray(per_mark), axis=0)
     res = {"timeline": {"kind": kind, "shapes": shapes, "columns": M, "family": fam, "code_object": which,

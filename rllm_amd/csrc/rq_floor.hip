@@ -111,11 +111,14 @@ __device__ __forceinline__ int floor_tile_c(const RqFloorTarget& T, int64_t tile
     return x;
 }
 
-// The target's chunk count picks the path (wave-uniform).
+// C = 0: the target's chunk count picks the path (wave-uniform; the mixed
+// q/k/v launch); otherwise every target has C chunks, which keeps the
+// registers (and the occupancy) those of one format.
+template <int C>
 __device__ __forceinline__ int floor_tile(const RqFloorTarget& T, int64_t tile, int lane, int& row) {
+    if (C != 0) return floor_tile_c<C == 0 ? 9 : C>(T, tile, lane, row);
     if (T.chunks == 9) return floor_tile_c<9>(T, tile, lane, row);
-    if (T.chunks == 13) return floor_tile_c<13>(T, tile, lane, row);
-    return floor_tile_c<17>(T, tile, lane, row);
+    return floor_tile_c<13>(T, tile, lane, row);
 }
 
 __device__ __forceinline__ void floor_store(const RqFloorTarget& T, int64_t tile, int lane, int row, int x) {
@@ -157,15 +160,16 @@ __device__ __forceinline__ RqFloorTarget floor_pick(const RqFloorParams& P, int 
     return r;
 }
 
-template <int THREADS, bool PAIR>
+template <int THREADS, bool PAIR, int C>
 __global__ __launch_bounds__(THREADS) void rq_floor_many_k(RqFloorParams P) {
     const int lane = threadIdx.x & 63;
-    const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // Wave-uniform (readfirstlane): the target pick and tile index stay scalar.
+    const int64_t gw = (int64_t)blockIdx.x * (THREADS / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (PAIR) {
         if (gw >= P.t[0].tiles) return;  // wave-uniform
         int r0, r1;
-        const int x0 = floor_tile(P.t[0], gw, lane, r0);
-        const int x1 = floor_tile(P.t[1], gw, lane, r1);
+        const int x0 = floor_tile<C>(P.t[0], gw, lane, r0);
+        const int x1 = floor_tile<C>(P.t[1], gw, lane, r1);
         floor_store(P.t[0], gw, lane, r0, x0);
         floor_store(P.t[1], gw, lane, r1, x1);
         return;
@@ -177,28 +181,32 @@ __global__ __launch_bounds__(THREADS) void rq_floor_many_k(RqFloorParams P) {
     const int64_t tile = gw - T.wave0;
     if (tile >= T.tiles) return;  // wave-uniform
     int row;
-    const int x = floor_tile(T, tile, lane, row);
+    const int x = floor_tile<C>(T, tile, lane, row);
     floor_store(T, tile, lane, row, x);
 }
 
 // Launches the general read floor: `count` targets one after the other in
 // the grid (or, with pair, two targets of equal tile counts side by side in
-// each wave), `threads` per workgroup (256, 512 or 1024). Returns a
+// each wave, 512 threads), `threads` per workgroup (256 or 1024). Targets of
+// different chunk counts only as Q4_K + Q6_K at 256 threads. Returns a
 // hipError_t.
 extern "C" int rq_floor_read_many(const void* targets, int count, int pair, int threads, void* stream) {
     if (!targets || count < 1 || count > 3 || (pair && (count != 2 || threads != 512)) ||
-        (threads != 256 && threads != 512 && threads != 1024))
+        (!pair && threads != 256 && threads != 1024))
         return (int)hipErrorInvalidValue;
     RqFloorParams P;
     memset(&P, 0, sizeof P);
     memcpy(P.t, targets, sizeof(RqFloorTarget) * count);
     int64_t waves = 0;
+    int c0 = ((const RqFloorTarget*)targets)[0].chunks;
+    bool same = true;
     for (int i = 0; i < count; i++) {
         RqFloorTarget& T = P.t[i];
         if (!T.base || !T.out || T.tiles <= 0 || T.rows <= 0 || T.R < 1 || T.R > 64 || (T.R & (T.R - 1)) ||
             T.S < 1 || T.S > 64 || (T.R > 1 && T.S > 64 / T.R) || T.rows > T.tiles * T.R ||
             (T.chunks != 9 && T.chunks != 13 && T.chunks != 17) || ((uintptr_t)T.base & 15))
             return (int)hipErrorInvalidValue;
+        same = same && T.chunks == c0;
         T.wave0 = pair ? 0 : waves;
         waves = pair ? T.tiles : waves + T.tiles;
     }
@@ -208,14 +216,35 @@ extern "C" int rq_floor_read_many(const void* targets, int count, int pair, int 
     const int wpg = threads / 64;
     const dim3 grid((unsigned)((waves + wpg - 1) / wpg)), block(threads);
     hipStream_t s = (hipStream_t)stream;
-    if (pair)
-        hipLaunchKernelGGL((rq_floor_many_k<512, true>), grid, block, 0, s, P);
+    // Launch shapes of the decode step: one format per launch (9, 13 or 17
+    // chunks) at 256 or 1024 threads, the mixed Q4_K / Q6_K one at 256, the
+    // gated FFN's pairs (Q4_K, Q4_0: 9; Q6_K: 13) at 512.
+    if (!same && (c0 + ((const RqFloorTarget*)targets)[count - 1].chunks != 22 || threads != 256 || pair))
+        return (int)hipErrorInvalidValue;
+#define RQ_FLOOR_LAUNCH(TH, PR, CC) hipLaunchKernelGGL((rq_floor_many_k<TH, PR, CC>), grid, block, 0, s, P)
+    if (!same)
+        RQ_FLOOR_LAUNCH(256, false, 0);
+    else if (pair && c0 == 9)
+        RQ_FLOOR_LAUNCH(512, true, 9);
+    else if (pair && c0 == 13)
+        RQ_FLOOR_LAUNCH(512, true, 13);
+    else if (pair)
+        return (int)hipErrorInvalidValue;
+    else if (threads == 256 && c0 == 9)
+        RQ_FLOOR_LAUNCH(256, false, 9);
+    else if (threads == 256 && c0 == 13)
+        RQ_FLOOR_LAUNCH(256, false, 13);
     else if (threads == 256)
-        hipLaunchKernelGGL((rq_floor_many_k<256, false>), grid, block, 0, s, P);
-    else if (threads == 512)
-        hipLaunchKernelGGL((rq_floor_many_k<512, false>), grid, block, 0, s, P);
+        RQ_FLOOR_LAUNCH(256, false, 17);
+    else if (threads == 1024 && c0 == 9)
+        RQ_FLOOR_LAUNCH(1024, false, 9);
+    else if (threads == 1024 && c0 == 13)
+        RQ_FLOOR_LAUNCH(1024, false, 13);
+    else if (threads == 1024)
+        RQ_FLOOR_LAUNCH(1024, false, 17);
     else
-        hipLaunchKernelGGL((rq_floor_many_k<1024, false>), grid, block, 0, s, P);
+        return (int)hipErrorInvalidValue;
+#undef RQ_FLOOR_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -391,19 +391,16 @@ struct TileLane {
 
 // part: the wave's k-part of an R = 1 tile split over several waves (its
 // first super-block is 64 part; padding lanes re-read that one).
+// Branch-free (it runs in every wave's preamble, ahead of the first load):
+// with sh = log2(Sp) (6 for R = 1), row = lane >> sh and the lane's column
+// in its row is lane mod Sp (R > 1, part 0) or 64 part + lane (R = 1).
 __device__ __forceinline__ TileLane tile_lane(const RqTiled& w, int lane, int part = 0) {
     TileLane r;
-    if (w.R > 1) {
-        const int sh = 6 - __builtin_ctz(w.R);  // log2(Sp): R is a power of two
-        r.row = lane >> sh;
-        r.col = lane & ((1 << sh) - 1);
-        r.real = r.col < w.S;
-        if (!r.real) r.col = 0;
-    } else {
-        r.row = 0;
-        r.real = 64 * part + lane < w.S;
-        r.col = 64 * part + (r.real ? lane : 0);
-    }
+    const int sh = 6 - __builtin_ctz(w.R);  // log2(Sp): R is a power of two
+    r.row = lane >> sh;
+    const int col = (lane & ((1 << sh) - 1)) + 64 * part;
+    r.real = col < w.S;
+    r.col = r.real ? col : 64 * part;
     r.slot = r.row * w.S + r.col;
     return r;
 }
@@ -731,14 +728,33 @@ __device__ __forceinline__ void stage_columns(const int8_t* xq, const u16* xd, c
     __syncthreads();
 }
 
-// Target ti of a launch (see sgpr_value).
+// Target ti of a launch (see sgpr_value). Every candidate field goes
+// through sgpr_value first, so all of them are in the one batch of parameter
+// loads; launches of one target (most of them) then skip the selects, on a
+// uniform branch (each select adds scalar instructions to every wave's
+// preamble, and a CU's waves issue those through one scalar unit before
+// their first load).
 __device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
+    RqMvTarget a, b, c;
+#define RQ_LOAD(f)              \
+    a.f = sgpr_value(P.t[0].f); \
+    b.f = sgpr_value(P.t[1].f); \
+    c.f = sgpr_value(P.t[2].f);
+    RQ_LOAD(w.main)
+    RQ_LOAD(w.tail)
+    RQ_LOAD(w.S)
+    RQ_LOAD(w.R)
+    RQ_LOAD(w.T)
+    RQ_LOAD(w.k)
+    RQ_LOAD(w.fmt)
+    RQ_LOAD(w.P)
+    RQ_LOAD(out)
+    RQ_LOAD(n)
+    RQ_LOAD(wave_start)
+#undef RQ_LOAD
+    if (P.count == 1) return a;
     RqMvTarget r;
-#define RQ_PICK(f)                                                                                        \
-    {                                                                                                     \
-        const auto a = sgpr_value(P.t[0].f), b = sgpr_value(P.t[1].f), c = sgpr_value(P.t[2].f);          \
-        r.f = ti == 0 ? a : (ti == 1 ? b : c);                                                            \
-    }
+#define RQ_PICK(f) r.f = ti == 0 ? a.f : (ti == 1 ? b.f : c.f);
     RQ_PICK(w.main)
     RQ_PICK(w.tail)
     RQ_PICK(w.S)
@@ -759,7 +775,8 @@ __device__ __forceinline__ RqMvTarget pick_target(const RqMvParams& P, int ti) {
 template <int FMT, int NC, bool F32IN, int WAVES, bool KP = false>
 __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     // Timeline marks (librq_tl.so only): 0 start, 1 weight loads issued,
-    // 2 staging done, 3 arithmetic done, 4 row sums stored.
+    // 2 staging done, 3 arithmetic done, 4 row sums stored, 5 preamble done
+    // (parameters loaded, target picked, addresses worked out).
     RqTl tlm;
     tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
@@ -792,17 +809,20 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
     const int tc = has_tile ? t : T.w.T - 1;
     const int slots = T.w.R * S;  // stored slots per tile
     const TileLane tl = tile_lane(T.w, lane, part);
-    const RowDst dst = row_dst(T, t, lane);
 
     // The tile's weight loads go out right behind round 0 of the staging loads.
     SB<FMT> w;
     constexpr bool ORDER = NC == 1 && !KP && FMT != RQ_FMT_Q8_0;
+    tl_mark(tlm, 5);
     stage_columns<FMT, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] {
         load_sb<FMT, ORDER>(T.w, tc, tl.slot, w);
         tl_mark(tlm, 1);
     });
     tl_mark(tlm, 2);
     if (!has_tile && kp == 1) return;  // wave-uniform; no barrier follows
+    // The row destination is worked out here, while the weights are on their
+    // way (before the loads it lengthened every wave's preamble).
+    const RowDst dst = row_dst(T, t, lane);
 
     float acc[NC];
 #pragma unroll
@@ -879,7 +899,8 @@ __device__ __forceinline__ void mvx_body(const RqMvParams& P) {
 template <int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     // Timeline marks (librq_tl.so only), as mvx_body's: 0 start, 1 weight
-    // loads issued, 2 staging done, 3 arithmetic done, 4 row sums stored.
+    // loads issued, 2 staging done, 3 arithmetic done, 4 row sums stored,
+    // 5 preamble done.
     RqTl tlm;
     tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
@@ -894,7 +915,6 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const bool has_tile = t < T.w.T;
     const int slots = T.w.R * S;
     const TileLane tl = tile_lane(T.w, lane);
-    const RowDst dst = row_dst(T, t, lane);
 
     SB<RQ_FMT_Q6_K> w;  // Q4_K: chunks 0..8
     // Chunk c of a slot lies at the same offset from the tile's start in
@@ -930,12 +950,14 @@ __device__ __forceinline__ void mvx_mix_body(const RqMvParams& P) {
     const int8_t* xq = F32IN ? nullptr : sgpr_value(P.xq);  // first kernarg batch (as mvx_body)
     const u16* xd = F32IN ? nullptr : sgpr_value(P.xd);
     const float* xf = F32IN ? sgpr_value(P.xf) : nullptr;
+    tl_mark(tlm, 5);
     stage_columns<RQ_FMT_MIX_K, NC, F32IN, WAVES, NC == 1>(xq, xd, xf, S, k, [&] {
         load(has_tile ? t : T.w.T - 1, tl.slot);
         tl_mark(tlm, 1);
     });
     tl_mark(tlm, 2);
     if (!has_tile) return;
+    const RowDst dst = row_dst(T, t, lane);  // while the weights are on their way
 
     float acc[NC];
 #pragma unroll
