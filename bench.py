@@ -424,6 +424,11 @@ def bench_decode(torch, gpu, orc, steps, warmup, m=1, family=None, variants=(Tru
     from rllm_amd.backend import HostTensor
     from rllm_amd.dtype import DType
 
+    # The earlier legs' freed buffers go back to the driver first, as in a
+    # serving process that loads its model before anything else: with them
+    # held in torch's cache (1 GiB of flush buffer, the floors' rotating
+    # copies) the step ran 4% slower (1090 -> 1133 us on one box).
+    torch.cuda.empty_cache()
     if family:
         gpu.set_kernels(family)
     t0 = time.time()
@@ -562,7 +567,15 @@ COUNTER_PASSES = [
     ["TCC_EA0_RDREQ_DRAM_32B_sum", "TCC_BUBBLE_sum"],
     ["FETCH_SIZE"],
     ["WRITE_SIZE"],
+    # A duration that does not come from the tracer's timestamps: the GRBM's
+    # busy cycles per dispatch, converted to time by the spin kernels of
+    # known length that the traffic child launches after the matvecs.
+    ["GRBM_GUI_ACTIVE", "GRBM_COUNT"],
 ]
+# The calibration spins: SPIN_TICKS of the 100 MHz real-time counter each,
+# SPIN_REPS launches of each length on one workgroup per CU.
+SPIN_TICKS = (2000, 4000)
+SPIN_REPS = 4
 
 
 def headline_kernel(name: str) -> bool:
@@ -598,6 +611,18 @@ def traffic_child(argv) -> int:
     for i in range(64):
         gpu.matvec(xq, ws[i % copies], out, M)
     torch.cuda.synchronize()
+    from rllm_amd import build as rq_build
+
+    if os.path.exists(rq_build.FLOOR_LIB):
+        L = ctypes.CDLL(rq_build.FLOOR_LIB)
+        L.rq_floor_spin.restype = ctypes.c_int
+        L.rq_floor_spin.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p]
+        for ticks in SPIN_TICKS:
+            for _ in range(SPIN_REPS):
+                rc = L.rq_floor_spin(ticks, gpu.compute_units, gpu.stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"rq_floor_spin: hipError {rc}")
+        torch.cuda.synchronize()
     for w in ws:
         w.free()
     gpu.close()
@@ -672,7 +697,6 @@ def timeline(argv) -> int:
     _, g = time_graph(torch, gpu, launch, chunk, 1, 2)
     buf = np.zeros(slots * marks, dtype=np.uint64)
     per_mark, spans, which = [], [], None
-    last_mark = {False: -1, True: MARKS_MV.index("stored")}  # the span ends at the final store
     for _ in range(replays):
         g.replay()
         torch.cuda.synchronize()
@@ -686,15 +710,19 @@ def timeline(argv) -> int:
         if which is None:
             raise RuntimeError("no instrumented kernel ran (the timeline covers rq_mvx*, rq_glu*, rq_mmq_*_16x*)")
         names = MARKS_GLU if kind == "glu" else (MARKS_MV if which == 0 else MARKS_MMQT)
-        rel = (live[:, :len(names)].astype(np.int64) - int(live[:, 0].min())) * 0.01  # 100 MHz ticks -> us
-        spans.append(float(rel[:, last_mark[names is MARKS_MV]].max()))
-        per_mark.append([[float(np.percentile(rel[:, i], q)) for q in (10, 50, 90, 100)] for i in range(len(names))])
+        # Stamps of 0 are marks the kernel did not reach (an MFMA launch of
+        # one column group has no group-1 marks).
+        sel = live[:, :len(names)]
+        rel = np.where(sel != 0, (sel.astype(np.int64) - int(live[:, 0].min())) * 0.01, np.nan)  # 100 MHz ticks -> us
+        spans.append(float(np.nanmax(rel)))  # first wave start to the last mark of any wave
+        per_mark.append([[float(np.nanpercentile(rel[:, i], q)) if np.isfinite(rel[:, i]).any() else float("nan")
+                          for q in (10, 50, 90, 100)] for i in range(len(names))])
     pm = np.median(np.asarray(per_mark), axis=0)
     res = {"timeline": {"kind": kind, "shapes": shapes, "columns": M, "family": fam, "code_object": which,
                         "waves": int(live.shape[0]), "replays": replays, "launches_per_replay": chunk,
                         "span_us": round(float(np.median(spans)), 3),
                         "marks_us": {n: {"p10": round(r[0], 3), "p50": round(r[1], 3), "p90": round(r[2], 3),
-                                         "max": round(r[3], 3)} for n, r in zip(names, pm)}}}
+                                         "max": round(r[3], 3)} for n, r in zip(names, pm) if np.isfinite(r).all()}}}
     print(json.dumps(res), flush=True)
     del g
     for wl in ws:
@@ -736,7 +764,7 @@ def measure_traffic() -> dict | None:
 
     if not shutil.which("rocprofv3"):
         return None
-    kern, copy = {}, {}
+    kern, copy, spin = {}, {}, {}
     for counters in COUNTER_PASSES:
         with tempfile.TemporaryDirectory() as d:
             cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", *counters, "--output-format", "csv", "-d", d,
@@ -748,6 +776,13 @@ def measure_traffic() -> dict | None:
                 return None
             rows = list(csv.DictReader(open(files[0])))
         for c in counters:
+            if c.startswith("GRBM_"):
+                # Spin dispatches in launch order: SPIN_REPS of each length.
+                sv = [(int(x.get("Dispatch_Id") or i), float(x["Counter_Value"])) for i, x in enumerate(rows)
+                      if x["Counter_Name"] == c and x["Kernel_Name"].startswith("rq_floor_spin_k")]
+                sv = [v for _, v in sorted(sv)]
+                if len(sv) == SPIN_REPS * len(SPIN_TICKS):
+                    spin[c] = [statistics.median(sv[i * SPIN_REPS:(i + 1) * SPIN_REPS]) for i in range(len(SPIN_TICKS))]
             kv = [float(x["Counter_Value"]) for x in rows if x["Counter_Name"] == c and headline_kernel(x["Kernel_Name"])]
             cv = [float(x["Counter_Value"]) for x in rows if x["Counter_Name"] == c and "copyBuffer" in x["Kernel_Name"]]
             if not kv or not cv:
@@ -758,11 +793,60 @@ def measure_traffic() -> dict | None:
     def read_bytes(v):
         return 32 * v["TCC_EA0_RDREQ_32B_sum"] + 64 * v["TCC_EA0_RDREQ_64B_sum"] + 128 * v["TCC_EA0_RDREQ_128B_sum"]
 
-    return {"bytes": read_bytes(kern) + kern["WRITE_SIZE"] * 1024, "read": read_bytes(kern),
+    busy = None
+    if "GRBM_GUI_ACTIVE" in spin:
+        # Counter cycles per us from the two spin lengths' difference; the
+        # line's intercept at zero length is what a dispatch counts beyond
+        # its waves' run under the profiler (its counter window, the spin's
+        # own ramp), which comes off the matvec's count too.
+        s_lo, s_hi = spin["GRBM_GUI_ACTIVE"]
+        per_us = (s_hi - s_lo) / ((SPIN_TICKS[1] - SPIN_TICKS[0]) / 100.0)
+        if per_us > 0:
+            base = s_lo - per_us * SPIN_TICKS[0] / 100.0
+            busy = {"busy_us": (kern["GRBM_GUI_ACTIVE"] - base) / per_us, "raw_us": kern["GRBM_GUI_ACTIVE"] / per_us,
+                    "overhead_us": base / per_us, "cycles_per_us": per_us, "gui_active": kern["GRBM_GUI_ACTIVE"],
+                    "grbm_count": kern["GRBM_COUNT"], "spin_gui_active": spin["GRBM_GUI_ACTIVE"],
+                    "spin_ticks": list(SPIN_TICKS)}
+    return {"busy": busy, "bytes": read_bytes(kern) + kern["WRITE_SIZE"] * 1024, "read": read_bytes(kern),
             "write": kern["WRITE_SIZE"] * 1024, "dram_read": 32 * kern["TCC_EA0_RDREQ_DRAM_32B_sum"],
             "fetch_size": kern["FETCH_SIZE"] * 1024, "counters": kern,
             "copy_check": {"bytes": COPY_BYTES, "read": read_bytes(copy), "write": copy["WRITE_SIZE"] * 1024,
                            "fetch_size": copy["FETCH_SIZE"] * 1024, "dram_read": 32 * copy["TCC_EA0_RDREQ_DRAM_32B_sum"]}}
+
+
+def measure_trace(steps: int, warmup: int) -> dict | None:
+    """The headline leg alone (bench.py --headline-only) under rocprofv3
+    --kernel-trace, in a child process: the traced kernel durations of its
+    launches (mean and median) beside the event-timed period per launch that
+    the traced child measures itself. The tracer adds a completion signal
+    per dispatch, which lengthens both; None if rocprofv3 is unavailable or
+    the child fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    if not shutil.which("rocprofv3"):
+        return None
+    with tempfile.TemporaryDirectory() as d:
+        cmd = ["timeout", "-s", "KILL", "180", "rocprofv3", "--kernel-trace", "--output-format", "csv", "-d", d, "-o",
+               "run", "--", sys.executable, os.path.abspath(__file__), "--headline-only", "--steps", str(steps),
+               "--warmup", str(warmup)]
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, cwd=d)
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs if f.endswith("kernel_trace.csv")]
+        if r.returncode != 0 or not files:
+            log(f"trace: rocprofv3 --kernel-trace failed ({r.returncode}): {r.stderr[-500:]}")
+            return None
+        rows = list(csv.DictReader(open(files[0])))
+    durs = [(int(x["End_Timestamp"]) - int(x["Start_Timestamp"])) / 1e3 for x in rows if headline_kernel(x["Kernel_Name"])]
+    try:
+        child = json.loads(r.stdout.strip().splitlines()[-1])
+    except (ValueError, IndexError):
+        return None
+    if not durs:
+        return None
+    return {"launches": len(durs), "mean_us": statistics.fmean(durs), "median_us": statistics.median(durs),
+            "period_us": child["roofline"]["kernel_us"]}
 
 
 # ---- BASELINE config lines ---------------------------------------------------
@@ -813,6 +897,7 @@ def main() -> int:
     ap.add_argument("--all-configs", action="store_true",
                     help="also the sweeps (both families at 1-32 columns, Q6_K batches, shard shapes, batch decode)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--no-trace", action="store_true", help="skip the rocprofv3 --kernel-trace child of the headline leg")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the headline leg (its graph replays and nothing else: no floors, cold launch, "
                          "traffic, configs, decode or CPU baseline), so that a kernel trace holds only its launches")
@@ -828,9 +913,13 @@ def main() -> int:
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
     if args.headline_only:
-        args.no_traffic = args.no_configs = args.no_decode = args.no_cpu = True
+        args.no_traffic = args.no_trace = args.no_configs = args.no_decode = args.no_cpu = True
         args.all_configs = False
     traffic = None if args.no_traffic else measure_traffic()
+    trace = None if args.no_trace else measure_trace(args.steps, args.warmup)
+    if trace:
+        log(f"trace: headline leg alone under --kernel-trace: {trace['launches']} launches, traced duration median "
+            f"{trace['median_us']:.3f} us (mean {trace['mean_us']:.3f}); that run's event period {trace['period_us']:.3f} us")
     # The headline launch's own span (first wave start to last store) from
     # the per-wave timeline of the instrumented build, in a child process.
     tl = None if args.headline_only else measure_timeline(["matvec", str(HEADLINE[0]), str(HEADLINE[1]),
@@ -843,6 +932,11 @@ def main() -> int:
         log(f"traffic: {traffic['bytes'] / 1e6:.2f} MB per launch: read {traffic['read']:.0f} B (DRAM "
             f"{traffic['dram_read']:.0f} B, FETCH_SIZE {traffic['fetch_size']:.0f} B), write {traffic['write']:.0f} B; "
             f"64 MiB copy reads {traffic['copy_check']['read']:.0f} B")
+        if traffic["busy"]:
+            b_ = traffic["busy"]
+            log(f"busy: GRBM_GUI_ACTIVE {b_['gui_active']:.0f} per launch at {b_['cycles_per_us']:.1f} per us (spins "
+                f"{b_['spin_gui_active']}): {b_['raw_us']:.3f} us, less {b_['overhead_us']:.3f} us per dispatch = "
+                f"{b_['busy_us']:.3f} us")
 
     import torch
 
@@ -994,6 +1088,18 @@ def main() -> int:
                          "fetch_size_raw": round(traffic["fetch_size"]),
                          "counters": {k_: round(v) for k_, v in traffic["counters"].items()},
                          "copy_check": {k_: round(v) for k_, v in traffic["copy_check"].items()}})
+    if trace:
+        # The same leg traced in a child: the tracer's durations, and the
+        # period it stretches to with its per-dispatch completion signals.
+        roofline.update({"traced_us": round(trace["median_us"], 3), "traced_mean_us": round(trace["mean_us"], 3),
+                         "traced_period_us": round(trace["period_us"], 3), "traced_launches": trace["launches"]})
+    if traffic and traffic["busy"]:
+        # GRBM busy time of one launch (counters, dispatches serialized by
+        # the profiler), converted with the spin kernels' cycles per us.
+        b_ = traffic["busy"]
+        roofline.update({"busy_us": round(b_["busy_us"], 3), "busy_raw_us": round(b_["raw_us"], 3),
+                         "busy_overhead_us": round(b_["overhead_us"], 3),
+                         "busy_cycles_per_us": round(b_["cycles_per_us"], 1)})
     if tl:
         # In-kernel span of the same launch (instrumented build, 100 MHz
         # real-time stamps): the period above less the gap between dependent

@@ -85,7 +85,7 @@ __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdg
 #define RQ_TL_MARKS 8
 #define RQ_TL_SLOTS 32768
 struct RqTl {
-    u64 t[RQ_TL_MARKS];
+    u64 t[RQ_TL_MARKS] = {};  // 0: mark not reached (a kernel's unused marks)
 };
 #ifdef RQ_TIMELINE
 __device__ u64 rq_tl[RQ_TL_SLOTS * RQ_TL_MARKS];

@@ -78,34 +78,27 @@ struct RqFloorTarget {
     int64_t wave0;   // first wave of the target (pair: 0 for both)
 };
 struct RqFloorParams {
-    RqFloorTarget t[3];
-    int32_t count;
+    int32_t count;  // first: loaded in the same batch as the targets
     int32_t pair;
+    RqFloorTarget t[3];
 };
 
 // One tile's loads (C chunks, unrolled and unguarded as the matvec issues
 // them, then the scale-plane word), folded with XOR.
 template <int C>
 __device__ __forceinline__ int floor_tile_c(const RqFloorTarget& T, int64_t tile, int lane, int& row) {
-    int col;
-    bool real;
-    if (T.R > 1) {
-        const int sh = 6 - __builtin_ctz(T.R);
-        row = lane >> sh;
-        col = lane & ((1 << sh) - 1);
-        real = col < T.S;
-    } else {
-        row = 0;
-        col = lane;
-        real = lane < T.S;
-    }
+    // The matvec's tile_lane: rows of 64 / R lanes (R = 1: the whole wave).
+    const int sh = 6 - __builtin_ctz(T.R);
+    row = lane >> sh;
+    const int col = lane & ((1 << sh) - 1);
+    const bool real = col < T.S;
     const int64_t slots = (int64_t)T.R * T.S;
     const int64_t slot = row * T.S + (real ? col : 0);
     const u8* p = T.base + (tile * C * slots + slot) * 16;
     int4 v[C];
 #pragma unroll
     for (int c = 0; c < C; c++) v[c] = ld16_nt(p + c * slots * 16);
-    int x = T.tail ? (int)*(const u16*)(T.tail + (tile * slots + slot) * 2) : 0;
+    int x = T.tail ? (int)*gmem((const u16*)(T.tail + (tile * slots + slot) * 2)) : 0;
 #pragma unroll
     for (int c = 0; c < C; c++) x ^= v[c].x ^ v[c].y ^ v[c].z ^ v[c].w;
     return x;
@@ -133,28 +126,36 @@ __device__ __forceinline__ void floor_store(const RqFloorTarget& T, int64_t tile
             (__builtin_amdgcn_readlane(x, 32) ^ __builtin_amdgcn_readlane(x, 48));
     const bool leader = g == 32 ? (lane & 31) == 16 : (g == 64 ? lane == 0 : (lane & (g - 1)) == 0);
     const int64_t r = tile * T.R + row;
-    if (leader && row < T.R && r < T.rows) T.out[r] = (u32)x;
+    if (leader && row < T.R && r < T.rows) gmem(T.out)[r] = (u32)x;
 }
 
-// Target ti by value (the matvec kernels' pick_target): a reference indexed
-// by the runtime target number would reload its fields with dependent
-// kernarg loads ahead of the first weight load.
-__device__ __forceinline__ RqFloorTarget floor_pick(const RqFloorParams& P, int ti) {
+// Every target's fields in one batch of kernarg loads (the matvec kernels'
+// pick_target): a reference indexed by the runtime target number would
+// reload its fields with dependent kernarg loads ahead of the first weight
+// load. floor_pick then takes the wave's target by value; a one-target
+// launch takes the first with no selects.
+__device__ __forceinline__ void floor_load(const RqFloorParams& P, RqFloorTarget& a, RqFloorTarget& b,
+                                           RqFloorTarget& c) {
+#define RQ_FLOAD(f)               \
+    a.f = sgpr_value(P.t[0].f); \
+    b.f = sgpr_value(P.t[1].f); \
+    c.f = sgpr_value(P.t[2].f);
+    RQ_FLOAD(base) RQ_FLOAD(tail) RQ_FLOAD(tiles) RQ_FLOAD(chunks) RQ_FLOAD(R) RQ_FLOAD(S) RQ_FLOAD(out)
+    RQ_FLOAD(rows) RQ_FLOAD(wave0)
+#undef RQ_FLOAD
+    a.pad = b.pad = c.pad = 0;
+}
+
+__device__ __forceinline__ RqFloorTarget floor_pick(const RqFloorParams& P, int64_t gw) {
+    RqFloorTarget a, b, c;
+    const int count = sgpr_value(P.count);
+    floor_load(P, a, b, c);
+    if (count == 1) return a;
+    const int ti = (int)(gw >= b.wave0) + (int)(gw >= c.wave0 && count > 2);
     RqFloorTarget r;
-#define RQ_FPICK(f)                                                                              \
-    {                                                                                            \
-        const auto a = sgpr_value(P.t[0].f), b = sgpr_value(P.t[1].f), c = sgpr_value(P.t[2].f); \
-        r.f = ti == 0 ? a : (ti == 1 ? b : c);                                                   \
-    }
-    RQ_FPICK(base)
-    RQ_FPICK(tail)
-    RQ_FPICK(tiles)
-    RQ_FPICK(chunks)
-    RQ_FPICK(R)
-    RQ_FPICK(S)
-    RQ_FPICK(out)
-    RQ_FPICK(rows)
-    RQ_FPICK(wave0)
+#define RQ_FPICK(f) r.f = ti == 0 ? a.f : (ti == 1 ? b.f : c.f);
+    RQ_FPICK(base) RQ_FPICK(tail) RQ_FPICK(tiles) RQ_FPICK(chunks) RQ_FPICK(R) RQ_FPICK(S) RQ_FPICK(out)
+    RQ_FPICK(rows) RQ_FPICK(wave0)
 #undef RQ_FPICK
     r.pad = 0;
     return r;
@@ -166,18 +167,17 @@ __global__ __launch_bounds__(THREADS) void rq_floor_many_k(RqFloorParams P) {
     // Wave-uniform (readfirstlane): the target pick and tile index stay scalar.
     const int64_t gw = (int64_t)blockIdx.x * (THREADS / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (PAIR) {
-        if (gw >= P.t[0].tiles) return;  // wave-uniform
+        RqFloorTarget A, B, unused;
+        floor_load(P, A, B, unused);
+        if (gw >= A.tiles) return;  // wave-uniform
         int r0, r1;
-        const int x0 = floor_tile<C>(P.t[0], gw, lane, r0);
-        const int x1 = floor_tile<C>(P.t[1], gw, lane, r1);
-        floor_store(P.t[0], gw, lane, r0, x0);
-        floor_store(P.t[1], gw, lane, r1, x1);
+        const int x0 = floor_tile<C>(A, gw, lane, r0);
+        const int x1 = floor_tile<C>(B, gw, lane, r1);
+        floor_store(A, gw, lane, r0, x0);
+        floor_store(B, gw, lane, r1, x1);
         return;
     }
-    int ti = 0;
-    if (P.count > 1 && gw >= P.t[1].wave0) ti = 1;
-    if (P.count > 2 && gw >= P.t[2].wave0) ti = 2;
-    const RqFloorTarget T = floor_pick(P, ti);
+    const RqFloorTarget T = floor_pick(P, gw);
     const int64_t tile = gw - T.wave0;
     if (tile >= T.tiles) return;  // wave-uniform
     int row;
@@ -255,5 +255,26 @@ __global__ __launch_bounds__(256) void rq_floor_empty_k() {}
 extern "C" int rq_floor_empty(int64_t workgroups, void* stream) {
     if (workgroups <= 0 || workgroups > 0x7fffffff) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(rq_floor_empty_k, dim3((unsigned)workgroups), dim3(256), 0, (hipStream_t)stream);
+    return (int)hipGetLastError();
+}
+
+// A kernel of known duration, which converts clock-cycle counters (rocprofv3
+// --pmc GRBM_GUI_ACTIVE) of other kernels to time: every wave reads the
+// 100 MHz real-time counter at its start and loops until it has advanced by
+// `ticks`, so the launch lasts `ticks` x 10 ns plus its ramp; two lengths
+// give the counter's cycles per microsecond as their difference. The wait
+// ends for every wave (the counter is free-running); no memory is written.
+__global__ __launch_bounds__(64) void rq_floor_spin_k(uint64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    uint64_t t = t0;
+    while (t - t0 < ticks) t = __builtin_amdgcn_s_memrealtime();
+}
+
+// Launches `workgroups` one-wave workgroups of rq_floor_spin_k that each run
+// `ticks` (1 .. 10^6, at most 10 ms) of the real-time counter. Returns a
+// hipError_t.
+extern "C" int rq_floor_spin(uint64_t ticks, int64_t workgroups, void* stream) {
+    if (ticks < 1 || ticks > 1000000 || workgroups <= 0 || workgroups > 65536) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rq_floor_spin_k, dim3((unsigned)workgroups), dim3(64), 0, (hipStream_t)stream, ticks);
     return (int)hipGetLastError();
 }
