@@ -357,20 +357,6 @@ __device__ __forceinline__ float sb_finish(const SBScale& sc, float accd, float 
     return accd;
 }
 
-// Dot of one super-block of a row with the activation super-block x[0..7].
-template <int FMT>
-__device__ __forceinline__ float sb_value(const SB<FMT>& w, const XJ* x) {
-    const SBScale sc = sb_scale<FMT>(w);
-    float accd = 0.f, accm = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        int s0, s1;
-        sub_dot<FMT>(w, j, x[j], s0, s1);
-        sub_accum<FMT>(sc, j, x[j], s0, s1, accd, accm);
-    }
-    return sb_finish<FMT>(sc, accd, accm);
-}
-
 // ---------------------------------------------------------------------------
 // Row reduction and store.
 
@@ -626,6 +612,15 @@ __device__ __forceinline__ void pin_sub(SB<FMT>& w, int j) {
     }
 }
 
+// The order in which a slot's sub-blocks are summed: Q6_K takes sub-block 6
+// (its pieces are all in by chunk 10) before 5 (chunks 11 and 12), so that a
+// one-column launch has two sub-blocks, not three, left after a slot's last
+// chunk; every column count sums in the same order.
+template <int FMT>
+__device__ __forceinline__ int sub_order(int jo) {
+    return FMT == RQ_FMT_Q6_K && (jo == 5 || jo == 6) ? 11 - jo : jo;
+}
+
 // Dot of one super-block slot with nc columns, accumulated into acc.
 template <int FMT, int NC>
 __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool active, float* acc) {
@@ -647,9 +642,10 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
             XJ xn;
             lds_read_x(rec, 0, xn);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
+            for (int jo = 0; jo < 8; jo++) {
+                const int j = sub_order<FMT>(jo);
                 const XJ x = xn;
-                if (j < 7) lds_read_x(rec, j + 1, xn);
+                if (jo < 7) lds_read_x(rec, sub_order<FMT>(jo + 1), xn);
                 pin_sub<FMT>(wp, j);
                 int s0, s1;
                 sub_dot<FMT>(wp, j, x, s0, s1);
@@ -658,7 +654,8 @@ __device__ __forceinline__ void slot_dot(const SB<FMT>& w, int S, int s, bool ac
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
+            for (int jo = 0; jo < 8; jo++) {
+                const int j = sub_order<FMT>(jo);  // as one column, so results do not depend on the column count
                 XJ x;
                 lds_read_x(rec, j, x);
                 int s0, s1;
@@ -1029,7 +1026,7 @@ template <int FMT, int NC, bool F32IN, int WAVES>
 __device__ __forceinline__ void glu_body(const RqGluParams& P) {
     // Timeline marks (librq_tl.so only): 0 start, 1 first tile's loads
     // issued, 2 staging done, 3 the wave's last tile's arithmetic done,
-    // 4 the block's g and u in LDS, 5 h and its Q8_1 stored.
+    // 4 the block's act(g) and u in LDS, 5 h and its Q8_1 stored.
     RqTl tlm;
     tl_mark(tlm, 0);
     const int lane = threadIdx.x & 63;
@@ -1071,8 +1068,12 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
         const int row = (q < NT ? q : q - NT) * R + rt;  // row within the block
 #pragma unroll
         for (int c = 0; c < NC; c++) {
+            // Gate rows leave act(g) (computed here, while the wave's next
+            // tile is still loading, rather than in the epilogue after the
+            // barrier, where it lengthened the launch's tail).
             const float v = group_sum(acc[c], g);
-            if (group_leader(lane, g) && rt < R) gu[((q < NT ? 0 : NC) + c) * 32 + row] = v;
+            const float o = q < NT ? act_apply(P.act, v) : v;
+            if (group_leader(lane, g) && rt < R) gu[((q < NT ? 0 : NC) + c) * 32 + row] = o;
         }
         w = wn;
         tl_mark(tlm, 3);
@@ -1088,7 +1089,7 @@ __device__ __forceinline__ void glu_body(const RqGluParams& P) {
         float h[4];
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            h[j] = act_apply(P.act, gu[c * 32 + 4 * f4 + j]) * gu[(NC + c) * 32 + 4 * f4 + j];
+            h[j] = gu[c * 32 + 4 * f4 + j] * gu[(NC + c) * 32 + 4 * f4 + j];  // act(g) * u
         const int64_t o = (int64_t)c * P.n + (int64_t)blk * 32;  // the block's first row (n % 32 == 0)
         if (P.hf && lane < 8) *(float4*)(P.hf + o + 4 * f4) = make_float4(h[0], h[1], h[2], h[3]);
         if (P.hq) q8_emit4(h, (o >> 2) + f4, lane < 8, P.hq, P.hd, P.hs);
