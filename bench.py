@@ -1024,8 +1024,9 @@ def main() -> int:
     if args.all_configs:
         plan = [("sweep", 12, 14336, 4096, m, fam) for m in (1, 2, 4, 8, 16, 32) for fam in ("dot4", "mfma")]
         plan += [("sweep", 14, 4096, 14336, m, fam) for m in (4, 8, 16, 32) for fam in ("dot4", "mfma")]
-        # 48 and 64 columns: one MFMA launch for Q4_K (16-column classes), two
-        # for Q6_K; the Q6_K head in the MFMA family at batch sizes.
+        # 48 and 64 columns: one MFMA launch, weights read once (Q4_K: the
+        # 16-column classes; Q6_K: 8 x 6 and 8 x 8); the Q6_K head in the MFMA
+        # family at batch sizes.
         plan += [("sweep", t, n, k, m, "mfma") for t, n, k in ((12, 14336, 4096), (14, 4096, 14336)) for m in (48, 64)]
         plan += [("sweep", 14, 128256, 4096, m, "mfma") for m in (4, 8, 16, 32)]
         # Prefill-size batches (the reference sends m > 8 to its MMQ or to

@@ -242,7 +242,7 @@ struct rq_ctx {
     hipFunction_t mmq[RQ_NUM_FMTS + 1][3][3] = {};
     hipFunction_t mmqf[RQ_NUM_FMTS + 1][3] = {};
     hipFunction_t mmqd[RQ_NUM_FMTS][3][3] = {};
-    hipFunction_t mmqg[RQ_NUM_FMTS + 1][2][3] = {};  // 8 x G columns, G = 2, 4
+    hipFunction_t mmqg[RQ_NUM_FMTS + 1][4][3] = {};  // 8 x G columns, G = 2, 4 (Q6_K also 6, 8)
     // 16 x G columns with four-activation entries (Q4_0, Q8_0, Q4_K; G = 1,
     // 2, 4; sbw 2, 4), and the same classes of the fused gate/up (sbw 4)
     hipFunction_t mmqt[RQ_NUM_FMTS][3][2] = {};
@@ -625,9 +625,14 @@ bool mmq_has_t(int fmt, int S2) { return fmt != RQ_FMT_MIX_K && (S2 + 3) / 4 <= 
 // Q6_K runs the 16-column kernels for up to 16 columns only: holding its
 // weights for a second group makes them spill.
 int mmqt_max_cols(int fmt) { return fmt == RQ_FMT_Q6_K ? 16 : 64; }
+// Q6_K takes up to 64 in its 8-column classes (8 x 6, 8 x 8 add each group's
+// k-parts as it ends, so LDS holds one group's partial sums next to 8 staged
+// columns of a 14336-wide row).
 int mmq_max_cols(int fmt, int S2) {
-    return mmq_np(fmt, S2) > 1 ? 8 : mmq_has_t(fmt, S2) && fmt != RQ_FMT_Q6_K ? 64 : 32;
+    return mmq_np(fmt, S2) > 1 ? 8 : (mmq_has_t(fmt, S2) || fmt == RQ_FMT_Q6_K) && fmt != RQ_FMT_MIX_K ? 64 : 32;
 }
+// Table index of an 8 x g class.
+int mmqg_index(int g) { return g == 2 ? 0 : g == 4 ? 1 : g == 6 ? 2 : 3; }
 // Group-count index of a 16-column class (g = 1, 2, 4).
 int mmqt_g_index(int g) { return g == 1 ? 0 : g == 2 ? 1 : 2; }
 // Super-blocks per wave of a 16-column launch: 4 for Q4_K; 2 for Q4_0 and
@@ -665,7 +670,7 @@ hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, const MmqPlan& L, bool f32_
         return ctx->mmqt[fmt][mmqt_g_index(L.g)][L.sbw == 2 ? 0 : 1];
     }
     const int si = mmq_sbw_index(L.sbw), mi = mmq_mp_index(L.mp), fi = mmq_fi(fmt);
-    if (L.g > 1) return ctx->mmqg[fi][L.g == 2 ? 0 : 1][si];
+    if (L.g > 1) return ctx->mmqg[fi][mmqg_index(L.g)][si];
     if (dots) return fmt == RQ_FMT_MIX_K ? nullptr : ctx->mmqd[fmt][mi][si];
     return f32_in ? ctx->mmqf[fi][si] : ctx->mmq[fi][mi][si];
 }
@@ -696,7 +701,8 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
     L.kxp = S2 * 256 + 64;  // 64 B of skew: columns start on different LDS banks
     L.pl_off = L.mp * L.kxp;
     L.part_off = L.pl_off + (mmq_planes(fmt) + (dots ? 1 : 0)) * L.mp * RQ_MMQ_NBP(S2) * 4;
-    L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * L.g * 4);
+    // Partial sums of every group, or (g > 4) of one group at a time.
+    L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * (L.g > 4 ? 1 : L.g) * 4);
 }
 
 // Launch geometry and LDS layout of an rq_mmq launch over weights of S2
@@ -806,7 +812,7 @@ MmqPlan mmq_cols(int fmt, int S2, int nc, bool allow16 = true) {
         return L;
     }
     L.mp = nc <= 1 ? 1 : nc <= 4 ? 4 : 8;
-    L.g = nc <= 8 ? 1 : (nc <= 16 ? 2 : 4);
+    L.g = nc <= 8 ? 1 : nc <= 16 ? 2 : nc <= 32 || fmt != RQ_FMT_Q6_K ? 4 : nc <= 48 ? 6 : 8;
     return L;
 }
 
@@ -838,7 +844,7 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     for (;;) {
         const int nc = (int)((m + ngroups - 1) / ngroups);
         const MmqPlan L = plan_for(nc);
-        if (L.lds <= ctx->lds_wide && (L.mp == 16 || nc <= 32)) break;
+        if (L.lds <= ctx->lds_wide && L.mp * L.g >= nc) break;
         if (nc == 1)
             return fail(RQ_ERR_SHAPE, "matvec: %lld columns too wide to stage (%d bytes of LDS)", (long long)k, L.lds);
         ngroups++;
@@ -1192,8 +1198,9 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
             if (kMmqSbw[si] > mmq_sbw_max(f)) continue;
             snprintf(name, sizeof name, "rq_mmqf_%s_%d", kFmtSuffix[f], kMmqSbw[si]);
             st = getm(ctx->mmq_mod, &ctx->mmqf[f][si], name);
-            for (int gi = 0; gi < 2 && st == RQ_OK; gi++) {
-                snprintf(name, sizeof name, "rq_mmq_%s_8x%d_%d", kFmtSuffix[f], 2 << gi, kMmqSbw[si]);
+            for (int gi = 0; gi < 4 && st == RQ_OK; gi++) {
+                if (gi >= 2 && (f != RQ_FMT_Q6_K || kMmqSbw[si] != 4)) continue;  // 8 x 6, 8 x 8: Q6_K only
+                snprintf(name, sizeof name, "rq_mmq_%s_8x%d_%d", kFmtSuffix[f], 2 * (gi + 1), kMmqSbw[si]);
                 st = getm(ctx->mmq_mod, &ctx->mmqg[f][gi][si], name);
             }
             for (int mi = 0; mi < 3 && st == RQ_OK; mi++) {

@@ -369,6 +369,33 @@ __device__ __forceinline__ void mmq_reduce(const RqMmqParams& P, const RqMmqTarg
     }
 }
 
+// Classes of more column groups than the LDS holds partial sums for (Q6_K 8 x
+// 6, 8 x 8: up to 64 columns over 14336-wide rows, whose staging of 8 columns
+// alone takes 115 KB) add each group's k-parts as soon as the group is done:
+// one partial slot per wave, reused by the next group after its staging
+// barrier. The sums and their order are mmq_reduce's.
+template <int G>
+struct GroupReduce {
+    static constexpr bool on = G > 4;
+};
+
+template <int MP, int NACC>
+__device__ __forceinline__ void mmq_reduce_group(const RqMmqParams& P, const RqMmqTarget& T, int gi) {
+    const int threads = blockDim.x, tid = threadIdx.x;
+    const int blk = blockIdx.x, ks = P.ks;
+    const float* part = (const float*)(mmq_lds + P.part_off);
+    __syncthreads();
+    float* out = (float*)T.out;
+    for (int it = tid; it < P.tr * MP * 16; it += threads) {
+        const int tl2 = it / (MP * 16), a = (it >> 4) % MP, nn = it & 15, ag = gi * MP + a;
+        const int tile2 = (blk - T.wg_start) * P.tr + tl2, row = tile2 * 16 + nn;
+        if (ag >= P.m || tile2 >= T.tiles || row >= T.n) continue;
+        float s = 0.f;
+        for (int q = 0; q < ks; q++) s += part_at<MP>(part, tl2 * ks + q, a, nn);
+        gmem(out)[(int64_t)ag * T.n + row] = s;
+    }
+}
+
 // rq_mmqglu_*: the workgroup's two tiles of gate (waves 0 .. ks tr - 1) and
 // of up (the next ks tr) meet as h = act(g) * u (act_apply, as rq_act_mul),
 // written as f32 (hf, when set) and, per column, as the Q8_1 block of the 32
@@ -1252,10 +1279,15 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     if (!DOTS) {
 #pragma unroll
         for (int e = 0; e < NACC; e++) y[e] *= 0.25f;
-        mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
+        if (GroupReduce<G>::on) {
+            mmq_part_store<MP, NACC>(P, y, wave, lane);
+            mmq_reduce_group<MP, NACC>(P, T, gi);
+        } else {
+            mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
+        }
     }
     }  // column groups
-    if (DOTS) return;
+    if (DOTS || GroupReduce<G>::on) return;
     if (GLU)
         mmq_reduce_glu<MP, G, NACC>(P, T);
     else
@@ -1442,6 +1474,8 @@ RQ_MMQ_SET(q4_k, RQ_FMT_Q4_K, 8)
 // Q6_K holds 48 B of codes per lane per super-block: sbw = 8 would need 96 registers of them.
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 2)
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 4)
+RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 6, 4)
+RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 8, 4)
 // Fused gate/up + activation + Q8_1 of the product (the reference's
 // mmq_glu_*), 4 super-blocks per wave (rows of up to 16: the two weights'
 // k-parts of two tiles fill at most 16 waves).

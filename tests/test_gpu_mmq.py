@@ -47,9 +47,19 @@ def _run(gpu, orc, t, n, k, m, seed, kind="random", dots=True):
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 32, 33, 48, 64, 65])
 def test_mmq_column_classes(mfma, orc, tname, m):
-    """Every column class (1, 4, 8 per launch; 8 x 2, 8 x 4; 16 x 1, 16 x 2,
-    16 x 4), padded classes and several launches."""
+    """Every column class (1, 4, 8 per launch; 8 x 2, 8 x 4, and for Q6_K
+    8 x 6, 8 x 8; 16 x 1, 16 x 2, 16 x 4), padded classes and several
+    launches."""
     _run(mfma, orc, MMQ_TYPES[tname], 45, 1024, m, 300 + m)
+
+
+@pytest.mark.parametrize("m", [33, 40, 48, 57, 64])
+def test_mmq_q6_k_wide_rows_many_columns(mfma, orc, m):
+    """Q6_K ffn_down's width (k = 14336) at 33 to 64 columns: one launch of
+    the 8 x 6 / 8 x 8 classes, which add each group's k-parts as it ends
+    (8 staged columns of this width leave no LDS for every group's partial
+    sums)."""
+    _run(mfma, orc, MMQ_TYPES["Q6_K"], 35, 14336, m, 14336 + m, kind="normal")
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
