@@ -91,6 +91,9 @@ _SIGNATURES = {
     "rq_matmul_many_noalloc": (_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                                       ctypes.POINTER(_i64), _int]),
     "rq_reserve": (_int, [_vp, _i64]),
+    "rq_set_gemm_min_m": (_int, [_vp, _i64]),
+    "rq_reserve_f16": (_int, [_vp, _i64, _i64]),
+    "rq_dequant_f16": (_int, [_vp, _vp, _vp, _i64]),
     "rq_block_dots": (_int, [_vp, ctypes.POINTER(Q8_1Struct), _i64, _vp, _vp, _i64]),
     "rq_set_kernels": (_int, [_vp, _int]),
     "rq_act_mul": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(Q8_1Struct)]),

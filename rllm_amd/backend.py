@@ -334,6 +334,22 @@ class HipBackend:
                                               w.data_ptr(), w.numel(), out.data_ptr(), out.numel(), rows, width, eps,
                                               ctypes.byref(q) if q is not None else None))
 
+    def set_gemm_min_m(self, m: int) -> None:
+        """Batched matmuls with at least m columns take the f16 GEMM route
+        (rq_set_gemm_min_m; 0: never)."""
+        _lib.check(_lib.lib().rq_set_gemm_min_m(self.ctx, m))
+
+    def reserve_f16(self, weight_values: int, x_values: int) -> None:
+        """Size the f16 GEMM route's scratches and create its BLAS handle
+        (call before capturing that route)."""
+        _lib.check(_lib.lib().rq_reserve_f16(self.ctx, weight_values, x_values))
+
+    def dequant_f16(self, w: HipWeight) -> torch.Tensor:
+        """The weight's elements as float16 [rows, cols] (rq_dequant_f16)."""
+        out = torch.empty((w.rows, w.cols), dtype=torch.float16, device=self.device)
+        _lib.check(_lib.lib().rq_dequant_f16(self.ctx, w.handle, out.data_ptr(), out.numel()))
+        return out
+
     def reserve(self, values: int) -> None:
         """Size the Q8_1 scratches (rq_matmul with m >= 2: values = m * k;
         rq_gated_ffn: values = m * n_ffn), so later calls allocate nothing

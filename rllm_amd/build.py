@@ -97,7 +97,7 @@ def _link(csrc: str, blob: str, static_obj: str, out: str, defines: list[str]) -
         "g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-Wextra", *defines,
         "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{csrc}",
         os.path.join(csrc, "rq_host.cpp"), os.path.join(csrc, "rq_gguf.cpp"), blob, static_obj,
-        f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+        f"-L{ROCM}/lib", "-lamdhip64", "-lrocblas", f"-Wl,-rpath,{ROCM}/lib",
         "-o", out,
     ]
 
