@@ -232,11 +232,11 @@ __device__ __forceinline__ void st16(void* p, int4 v) {
     *(__attribute__((address_space(1))) v4i_g*)p = v4i_g{v.x, v.y, v.z, v.w};
 }
 
-// The 32 f32 values y of one block as f16, 64 contiguous bytes at out
-// (16-byte aligned). Each value passes the empty asm first, as in f2h_mul:
-// fused into the conversion (v_fma_mix with a zero addend) a product would be
-// rounded once instead of twice, and a -0 product would come out as +0.
-__device__ __forceinline__ void put32_f16(u16* out, const float* y) {
+// The 32 f32 values y of one block as f16, four 16-byte pieces of 8 values.
+// Each value passes the empty asm first, as in f2h_mul: fused into the
+// conversion (v_fma_mix with a zero addend) a product would be rounded once
+// instead of twice, and a -0 product would come out as +0.
+__device__ __forceinline__ void pack32_f16(const float* y, int4* v) {
     u16 h[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) {
@@ -246,13 +246,22 @@ __device__ __forceinline__ void put32_f16(u16* out, const float* y) {
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        int4 v;
-        v.x = (int)((u32)h[8 * i] | ((u32)h[8 * i + 1] << 16));
-        v.y = (int)((u32)h[8 * i + 2] | ((u32)h[8 * i + 3] << 16));
-        v.z = (int)((u32)h[8 * i + 4] | ((u32)h[8 * i + 5] << 16));
-        v.w = (int)((u32)h[8 * i + 6] | ((u32)h[8 * i + 7] << 16));
-        st16(out + 8 * i, v);
+        v[i].x = (int)((u32)h[8 * i] | ((u32)h[8 * i + 1] << 16));
+        v[i].y = (int)((u32)h[8 * i + 2] | ((u32)h[8 * i + 3] << 16));
+        v[i].z = (int)((u32)h[8 * i + 4] | ((u32)h[8 * i + 5] << 16));
+        v[i].w = (int)((u32)h[8 * i + 6] | ((u32)h[8 * i + 7] << 16));
     }
+}
+
+// LDS staging of a workgroup's f16 blocks (the f16 dequantization): a
+// thread's block goes in as four pieces, piece q into plane q at the thread's
+// slot; the planes are one slot longer than a workgroup so that the pieces
+// of one slot sit in different banks. Stores then write 16 contiguous bytes
+// per lane.
+constexpr int kF16Plane = RQ_THREADS + 1;
+__device__ __forceinline__ void stage_f16(int4* lds, int slot, const int4* v) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) lds[q * kF16Plane + slot] = v[q];
 }
 
 __device__ __forceinline__ u8 byte_at(const int4& v, int i) {

@@ -1855,8 +1855,11 @@ rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out) {
         p.tiles = w->tiles;
         f = ctx->mmq_dequant16[w->fmt];
     }
-    const int64_t items = w->rows * (w->cols / 32);
-    return launch(ctx, f, "rq_dequant16", (uint64_t)((items + RQ_THREADS - 1) / RQ_THREADS), &p);
+    // One thread per (row, 32-element block): the dot4 layout's blocks in
+    // row order, the MFMA layout's as workgroups of 16 blocks of one tile.
+    const int64_t U = w->cols / 32;
+    const int64_t grid = w->dot4 ? (w->rows * U + RQ_THREADS - 1) / RQ_THREADS : (int64_t)w->tiles * ((U + 15) / 16);
+    return launch(ctx, f, "rq_dequant16", (uint64_t)grid, &p);
 }
 
 rq_status gemm_route(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* const* ws, float* const* outs,
