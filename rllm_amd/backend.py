@@ -21,6 +21,10 @@ from . import _lib
 from .dtype import DType
 from .errors import ShapeError, UnsupportedError
 
+# rq_set_gemm_min_m's value at rq_open when RQ_GEMM_MIN_M is unset: batched
+# matmuls of 65 or more columns take the f16 GEMM route.
+GEMM_MIN_M_DEFAULT = 65
+
 
 @dataclass
 class HostTensor:
@@ -336,7 +340,7 @@ class HipBackend:
 
     def set_gemm_min_m(self, m: int) -> None:
         """Batched matmuls with at least m columns take the f16 GEMM route
-        (rq_set_gemm_min_m; 0: never)."""
+        (rq_set_gemm_min_m; 0: never; GEMM_MIN_M_DEFAULT unless set)."""
         _lib.check(_lib.lib().rq_set_gemm_min_m(self.ctx, m))
 
     def reserve_f16(self, weight_values: int, x_values: int) -> None:

@@ -263,7 +263,11 @@ struct rq_ctx {
     hipFunction_t dequant16[RQ_NUM_FMTS] = {};
     hipFunction_t mmq_dequant16[RQ_NUM_FMTS] = {};
     hipFunction_t f2h = nullptr;
-    int64_t gemm_min_m = 0;  // 0: never
+    // From 65 columns by default: the int8 MFMA launches take up to 64
+    // columns, and past that each further 64 reads the weights again, while
+    // the f16 route's cost grows slowly with m (Q4_K 14336x4096: int8 37 /
+    // 71 / 281 us at 64 / 96 / 512 columns, the route 55 / 56 / 93 us).
+    int64_t gemm_min_m = 65;  // 0: never
     rocblas_handle blas = nullptr;
     void* blas_ws = nullptr;
     uint16_t* w16 = nullptr;
@@ -1929,9 +1933,9 @@ rq_status matmul_many_run(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m,
     for (int i = 0; i < count; i++)
         if (!aligned(outs[i], 4)) return fail(RQ_ERR_INVALID, "matmul: output %d not 4-byte aligned", i);
     if ((st = bind(ctx)) != RQ_OK) return st;
-    // Prefill-size batches on request (rq_set_gemm_min_m): the f16 GEMM
-    // route. Never for rq_matmul_many_noalloc, whose point is to allocate
-    // nothing.
+    // Prefill-size batches (m >= rq_set_gemm_min_m's value, 65 unless set):
+    // the f16 GEMM route. Never for rq_matmul_many_noalloc, whose point is
+    // to allocate nothing.
     if (!fixed && ctx->gemm_min_m > 0 && m >= ctx->gemm_min_m) return gemm_route(ctx, x, m, ws, outs, count);
     // m == 1: each launch quantizes x while staging it (bit-identical to
     // rq_quantize_q8_1), saving the quantize launch. For m >= 2 the staging

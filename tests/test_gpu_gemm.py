@@ -13,13 +13,15 @@ librq plus rocBLAS gemm_ex with f32 output.
   too: the route rounds both operands to f16.
 - The route is deterministic and can be captured after rq_reserve_f16;
   rq_matmul_many_noalloc never takes it.
+- By default it starts at 65 columns: 64 columns stay on the int8 path,
+  65 take the route.
 """
 import numpy as np
 import pytest
 import torch
 
 from gpu_util import make_weight, upload
-from rllm_amd.backend import HipBackend
+from rllm_amd.backend import GEMM_MIN_M_DEFAULT, HipBackend
 from rllm_amd.errors import ShapeError
 
 pytestmark = pytest.mark.gpu
@@ -32,7 +34,7 @@ def route(gpuk):
     """`gpuk` (both kernel families) with every batched matmul on the f16 route."""
     gpuk.set_gemm_min_m(1)
     yield gpuk
-    gpuk.set_gemm_min_m(0)
+    gpuk.set_gemm_min_m(GEMM_MIN_M_DEFAULT)
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
@@ -102,9 +104,33 @@ def test_below_min_m_keeps_the_int8_path(gpu, orc):
         fixed = gpu.alloc(m * n)
         gpu.matmul_many_noalloc(x, [wg], [fixed], m)
     finally:
-        gpu.set_gemm_min_m(0)
+        gpu.set_gemm_min_m(GEMM_MIN_M_DEFAULT)
     assert torch.equal(below.view(torch.int32), ref.view(torch.int32))
     assert torch.equal(fixed.view(torch.int32), ref.view(torch.int32))
+
+
+def test_default_threshold(orc):
+    """A fresh context: 64 columns give the int8 path's bits, 65 the
+    route's."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    fresh = HipBackend(0)
+    try:
+        k, n = 4096, 48
+        w = make_weight(orc, 12, n, k, 61, "normal")
+        wg = upload(fresh, 12, w, n, k)
+        for m, route in ((GEMM_MIN_M_DEFAULT - 1, False), (GEMM_MIN_M_DEFAULT, True)):
+            x = fresh.from_host(orc.normal(62 + m, m * k))
+            got = fresh.alloc(m * n)
+            fresh.matmul(x, wg, got, m)
+            fresh.set_gemm_min_m(1 if route else 0)
+            want = fresh.alloc(m * n)
+            fresh.matmul(x, wg, want, m)
+            fresh.set_gemm_min_m(GEMM_MIN_M_DEFAULT)
+            assert torch.equal(got.view(torch.int32), want.view(torch.int32)), f"m={m}"
+    finally:
+        fresh.synchronize()
+        fresh.close()
 
 
 def _capture(gpu, fn):
@@ -121,6 +147,7 @@ def _capture(gpu, fn):
     return g
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_f16_route_graph_replays(orc):
     """A fresh context: capturing the route before rq_reserve_f16 is refused;
     after it, replays with new inputs equal eager calls bit for bit."""

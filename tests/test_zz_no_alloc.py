@@ -2,13 +2,16 @@
 library's fixed device array (no allocation). Its outputs must equal
 rq_matmul_many's bit for bit (same kernels, same quantization), on calls in a
 row whose inputs shrink (the array keeps the previous call's contents), in
-both kernel families; sizes over the array's capacity are refused."""
+both kernel families; sizes over the array's capacity are refused. It never
+takes the f16 GEMM route, so at 65 columns and more it is compared with
+rq_matmul_many held to the int8 path (rq_set_gemm_min_m 0)."""
 import numpy as np
 import pytest
 import torch
 
 from gpu_util import make_weight, upload
 from rllm_amd import _lib
+from rllm_amd.backend import GEMM_MIN_M_DEFAULT
 from rllm_amd.errors import ShapeError
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +59,11 @@ def test_noalloc_capacity(gpu, orc):
     out = gpu.alloc((m + 1) * n)
     gpu.matmul_many_noalloc(x, [w], [out], m)
     want = gpu.alloc(m * n)
-    gpu.matmul_many(x, [w], [want], m)
+    gpu.set_gemm_min_m(0)
+    try:
+        gpu.matmul_many(x, [w], [want], m)
+    finally:
+        gpu.set_gemm_min_m(GEMM_MIN_M_DEFAULT)
     assert torch.equal(out[:m * n].view(torch.int32), want.view(torch.int32))
     with pytest.raises(ShapeError, match="fixed scratch"):
         gpu.matmul_many_noalloc(x, [w], [out], m + 1)
