@@ -348,6 +348,11 @@ class HipBackend:
         (call before capturing that route)."""
         _lib.check(_lib.lib().rq_reserve_f16(self.ctx, weight_values, x_values))
 
+    def keep_f16(self, w: HipWeight) -> None:
+        """Give w a persistent f16 copy that the f16 GEMM route reads
+        instead of dequantizing it per call (rq_weight_keep_f16)."""
+        _lib.check(_lib.lib().rq_weight_keep_f16(self.ctx, w.handle))
+
     def dequant_f16(self, w: HipWeight) -> torch.Tensor:
         """The weight's elements as float16 [rows, cols] (rq_dequant_f16)."""
         out = torch.empty((w.rows, w.cols), dtype=torch.float16, device=self.device)

@@ -316,6 +316,9 @@ struct rq_weight {
     const uint8_t* hdr = nullptr;
     int32_t tiles = 0, S2 = 0;
     size_t code_bytes = 0, hdr_bytes = 0;
+    // Persistent f16 copy of the elements (rq_weight_keep_f16), read by the
+    // f16 GEMM route instead of dequantizing per call.
+    uint16_t* f16 = nullptr;
 };
 
 namespace {
@@ -1335,7 +1338,9 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         // handles stay for rq_weight_free, which then only deletes them.
         for (rq_weight* w : ctx->live) {
             if (w->base) (void)hipFree(w->base);
+            if (w->f16) (void)hipFree(w->f16);
             w->base = nullptr;
+            w->f16 = nullptr;
             w->ctx = nullptr;
         }
         if (ctx->sq) (void)hipFree(ctx->sq);
@@ -1584,6 +1589,10 @@ extern "C" rq_status rq_weight_free(rq_weight* w) {
         hipError_t e = hipFreeAsync(w->base, ctx->stream);
         if (e != hipSuccess) st = hip_fail("hipFreeAsync", e);
     }
+    if (st == RQ_OK && w->f16) {
+        hipError_t e = hipFreeAsync(w->f16, ctx->stream);
+        if (e != hipSuccess) st = hip_fail("hipFreeAsync", e);
+    }
     delete w;
     return st;
 }
@@ -1741,6 +1750,7 @@ namespace {
 rq_status ensure_blas(rq_ctx* ctx);
 rq_status grow_f16(rq_ctx* ctx, uint16_t** p, int64_t* cap, int64_t values);
 rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out);
+rq_status refuse_capture(rq_ctx* ctx, const char* what);
 }  // namespace
 
 extern "C" rq_status rq_set_gemm_min_m(rq_ctx* ctx, int64_t m) {
@@ -1759,6 +1769,23 @@ extern "C" rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t 
     if ((st = ensure_blas(ctx)) != RQ_OK) return st;
     if ((st = grow_f16(ctx, &ctx->w16, &ctx->w16_cap, weight_values)) != RQ_OK) return st;
     return grow_f16(ctx, &ctx->x16, &ctx->x16_cap, x_values);
+}
+
+extern "C" rq_status rq_weight_keep_f16(rq_ctx* ctx, rq_weight* w) {
+    if (!ctx) return fail(RQ_ERR_INVALID, "rq_weight_keep_f16: null context");
+    rq_status st = check_weight(ctx, w, "rq_weight_keep_f16");
+    if (st != RQ_OK) return st;
+    if (w->f16) return RQ_OK;
+    if ((st = bind(ctx)) != RQ_OK) return st;
+    if ((st = refuse_capture(ctx, "rq_weight_keep_f16 allocates")) != RQ_OK) return st;
+    uint16_t* p = nullptr;
+    HIP_TRY(hipMalloc((void**)&p, (size_t)(w->rows * w->cols) * 2));
+    if ((st = dequant16_launch(ctx, w, p)) != RQ_OK) {
+        (void)hipFree(p);
+        return st;
+    }
+    w->f16 = p;
+    return RQ_OK;
 }
 
 extern "C" rq_status rq_dequant_f16(rq_ctx* ctx, const rq_weight* w, uint16_t* out, int64_t out_len) {
@@ -1869,8 +1896,9 @@ rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out) {
 rq_status gemm_route(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* const* ws, float* const* outs,
                      int count) {
     const int64_t k = ws[0]->cols;
-    int64_t wmax = 0;
-    for (int i = 0; i < count; i++) wmax = std::max(wmax, ws[i]->rows * k);
+    int64_t wmax = 0;  // the largest weight without a persistent f16 copy
+    for (int i = 0; i < count; i++)
+        if (!ws[i]->f16) wmax = std::max(wmax, ws[i]->rows * k);
     rq_status st;
     if ((st = ensure_blas(ctx)) != RQ_OK) return st;
     if ((st = grow_f16(ctx, &ctx->x16, &ctx->x16_cap, m * k)) != RQ_OK) return st;
@@ -1884,11 +1912,15 @@ rq_status gemm_route(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* co
     const float alpha = 1.f, beta = 0.f;
     for (int i = 0; i < count; i++) {
         const rq_weight* w = ws[i];
-        if ((st = dequant16_launch(ctx, w, ctx->w16)) != RQ_OK) return st;
+        const uint16_t* a = w->f16;
+        if (!a) {
+            if ((st = dequant16_launch(ctx, w, ctx->w16)) != RQ_OK) return st;
+            a = ctx->w16;
+        }
         // Row-major out[m][rows] is the column-major rows x m product
         // W (column-major k x rows, transposed) times x (column-major k x m).
         bs = rocblas_gemm_ex(ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)w->rows,
-                             (rocblas_int)m, (rocblas_int)k, &alpha, ctx->w16, rocblas_datatype_f16_r, (rocblas_int)k,
+                             (rocblas_int)m, (rocblas_int)k, &alpha, a, rocblas_datatype_f16_r, (rocblas_int)k,
                              ctx->x16, rocblas_datatype_f16_r, (rocblas_int)k, &beta, outs[i], rocblas_datatype_f32_r,
                              (rocblas_int)w->rows, outs[i], rocblas_datatype_f32_r, (rocblas_int)w->rows,
                              rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);

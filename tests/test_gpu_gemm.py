@@ -15,6 +15,7 @@ librq plus rocBLAS gemm_ex with f32 output.
   rq_matmul_many_noalloc never takes it.
 - By default it starts at 65 columns: 64 columns stay on the int8 path,
   65 take the route.
+- A weight's persistent f16 copy (rq_weight_keep_f16) changes no bit.
 """
 import numpy as np
 import pytest
@@ -85,6 +86,26 @@ def test_matmul_many_f16_route_and_determinism(route, orc):
         one = route.alloc(m * n)
         route.matmul(x, wg, one, m)
         assert torch.equal(one.view(torch.int32), a.view(torch.int32)), f"type {t}: matmul_many differs from matmul"
+
+
+def test_keep_f16_gives_the_same_bits(route, orc):
+    """A persistent f16 copy (rq_weight_keep_f16) changes no result: the route
+    reads the same f16 values it would dequantize, alone and beside weights
+    without a copy in one matmul_many."""
+    k, m = 4096, 24
+    spec = [(12, 96), (14, 64)]
+    wgs = [upload(route, t, make_weight(orc, t, n, k, 900 + i, "normal"), n, k) for i, (t, n) in enumerate(spec)]
+    x = route.from_host(orc.normal(910, m * k))
+    before = [route.alloc(m * n) for _, n in spec]
+    route.matmul_many(x, wgs, before, m)
+    route.keep_f16(wgs[0])
+    route.keep_f16(wgs[0])  # a second call keeps the first copy
+    after = [route.alloc(m * n) for _, n in spec]
+    route.matmul_many(x, wgs, after, m)
+    for (t, _), a, b in zip(spec, before, after):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"type {t}"
+    for wg in wgs:
+        wg.free()
 
 
 def test_below_min_m_keeps_the_int8_path(gpu, orc):
