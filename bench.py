@@ -189,7 +189,7 @@ def bench_matmul_routes(torch, gpu, orc, t, n, k, m, steps, warmup, seed=7):
     xg = gpu.from_host(x)
     out = gpu.alloc(m * n)
     gpu.reserve(m * k)
-    gpu.reserve_f16(n * k, m * k)
+    gpu.reserve_f16(n * k, m * k, m * n)
     mc = 4
     qs, d, _ = orc.quantize_q8_1(x[:mc * k], mc, k)
     wants = {"int8": orc.matvec_q8_1(t, w, n, k, qs, d, mc), "f16 gemm": orc.cpu_matmul(t, w, n, k, x[:mc * k], mc)}

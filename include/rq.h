@@ -236,12 +236,13 @@ rq_status rq_reserve(rq_ctx* ctx, int64_t values);
  * it. */
 rq_status rq_set_gemm_min_m(rq_ctx* ctx, int64_t m);
 
-/* Sizes the f16 GEMM route's scratches (the largest weight, rows * cols
- * values; x, m * k values) and creates its BLAS handle with a fixed
- * workspace, so that later calls of the route allocate nothing (graph
- * capture). Calls that would grow a scratch while the stream is capturing
- * fail. */
-rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t x_values);
+/* Sizes the f16 GEMM route's scratches (the largest weight without a
+ * persistent f16 copy, rows * cols values; x, m * k values; the split-k
+ * partial products of the largest output, m * rows values) and creates its
+ * BLAS handle with a fixed workspace, so that later calls of the route
+ * allocate nothing (graph capture). Calls that would grow a scratch while
+ * the stream is capturing fail. */
+rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t x_values, int64_t out_values);
 
 /* Keeps a persistent f16 copy of the weight's elements (rows * cols * 2
  * bytes of device memory, freed with the weight), which the f16 GEMM route

@@ -343,10 +343,10 @@ class HipBackend:
         (rq_set_gemm_min_m; 0: never; GEMM_MIN_M_DEFAULT unless set)."""
         _lib.check(_lib.lib().rq_set_gemm_min_m(self.ctx, m))
 
-    def reserve_f16(self, weight_values: int, x_values: int) -> None:
-        """Size the f16 GEMM route's scratches and create its BLAS handle
-        (call before capturing that route)."""
-        _lib.check(_lib.lib().rq_reserve_f16(self.ctx, weight_values, x_values))
+    def reserve_f16(self, weight_values: int, x_values: int, out_values: int) -> None:
+        """Size the f16 GEMM route's scratches (rows * cols, m * k, m * rows
+        values) and create its BLAS handle (call before capturing that route)."""
+        _lib.check(_lib.lib().rq_reserve_f16(self.ctx, weight_values, x_values, out_values))
 
     def keep_f16(self, w: HipWeight) -> None:
         """Give w a persistent f16 copy that the f16 GEMM route reads

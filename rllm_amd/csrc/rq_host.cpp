@@ -115,6 +115,8 @@ constexpr int kLdsBudget = 64 << 10;
 constexpr int kLdsPerSb = 400;
 // Most waves of a dot4 matvec launch whose rows are split into k-parts.
 constexpr int64_t kKpMaxWaves = 4096;
+// Most k-slices of the f16 GEMM route's split-k products.
+constexpr int kMaxGemmSplits = 8;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -274,6 +276,12 @@ struct rq_ctx {
     int64_t w16_cap = 0;
     uint16_t* x16 = nullptr;
     int64_t x16_cap = 0;
+    // Split-k partial products (f32) and their sum kernel; gemm_splits > 0
+    // forces the split count (RQ_GEMM_SPLITS), 0 picks it per call.
+    hipFunction_t sum_parts = nullptr;
+    float* gparts = nullptr;
+    int64_t gparts_cap = 0;
+    int gemm_splits = 0;
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
     hipStream_t stream = nullptr;
@@ -1175,6 +1183,7 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     rq_status st = get(&ctx->quant, "rq_quantize_q8_1");
     if (st == RQ_OK) st = get(&ctx->act_mul, "rq_act_mul");
     if (st == RQ_OK) st = get(&ctx->f2h, "rq_f32_to_f16");
+    if (st == RQ_OK) st = get(&ctx->sum_parts, "rq_sum_parts");
     for (int i = 0; i < 4 && st == RQ_OK; i++) {
         char nname[32];
         snprintf(nname, sizeof nname, "rq_rms_norm_%d", 1 << i);
@@ -1297,6 +1306,7 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
     if (const char* v = getenv("RQ_MMQ_SBW")) ctx->mmq_sbw = atoi(v);
     if (const char* v = getenv("RQ_MMQ_TR")) ctx->mmq_tr = std::max(0, std::min(16, atoi(v)));
     if (const char* v = getenv("RQ_GEMM_MIN_M")) ctx->gemm_min_m = std::max(0ll, atoll(v));
+    if (const char* v = getenv("RQ_GEMM_SPLITS")) ctx->gemm_splits = std::max(0, std::min(kMaxGemmSplits, atoi(v)));
     *out = ctx;
     return RQ_OK;
 }
@@ -1353,6 +1363,7 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         if (ctx->blas_ws) (void)hipFree(ctx->blas_ws);
         if (ctx->w16) (void)hipFree(ctx->w16);
         if (ctx->x16) (void)hipFree(ctx->x16);
+        if (ctx->gparts) (void)hipFree(ctx->gparts);
         if (ctx->up_stream) (void)hipStreamSynchronize(ctx->up_stream);
         for (int b = 0; b < 2; b++) {
             if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
@@ -1751,6 +1762,7 @@ rq_status ensure_blas(rq_ctx* ctx);
 rq_status grow_f16(rq_ctx* ctx, uint16_t** p, int64_t* cap, int64_t values);
 rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out);
 rq_status refuse_capture(rq_ctx* ctx, const char* what);
+rq_status grow_parts(rq_ctx* ctx, int64_t values);
 }  // namespace
 
 extern "C" rq_status rq_set_gemm_min_m(rq_ctx* ctx, int64_t m) {
@@ -1760,15 +1772,17 @@ extern "C" rq_status rq_set_gemm_min_m(rq_ctx* ctx, int64_t m) {
     return RQ_OK;
 }
 
-extern "C" rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t x_values) {
+extern "C" rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t x_values, int64_t out_values) {
     if (!ctx) return fail(RQ_ERR_INVALID, "rq_reserve_f16: null context");
-    if (weight_values < 0 || x_values < 0)
-        return fail(RQ_ERR_SHAPE, "rq_reserve_f16: %lld, %lld values", (long long)weight_values, (long long)x_values);
+    if (weight_values < 0 || x_values < 0 || out_values < 0)
+        return fail(RQ_ERR_SHAPE, "rq_reserve_f16: %lld, %lld, %lld values", (long long)weight_values,
+                    (long long)x_values, (long long)out_values);
     rq_status st = bind(ctx);
     if (st != RQ_OK) return st;
     if ((st = ensure_blas(ctx)) != RQ_OK) return st;
     if ((st = grow_f16(ctx, &ctx->w16, &ctx->w16_cap, weight_values)) != RQ_OK) return st;
-    return grow_f16(ctx, &ctx->x16, &ctx->x16_cap, x_values);
+    if ((st = grow_f16(ctx, &ctx->x16, &ctx->x16_cap, x_values)) != RQ_OK) return st;
+    return grow_parts(ctx, kMaxGemmSplits * ((out_values + 3) & ~int64_t(3)));
 }
 
 extern "C" rq_status rq_weight_keep_f16(rq_ctx* ctx, rq_weight* w) {
@@ -1867,6 +1881,40 @@ rq_status grow_f16(rq_ctx* ctx, uint16_t** p, int64_t* cap, int64_t values) {
     return RQ_OK;
 }
 
+rq_status grow_parts(rq_ctx* ctx, int64_t values) {
+    if (values <= ctx->gparts_cap) return RQ_OK;
+    rq_status st = refuse_capture(ctx, "split-k scratch too small");
+    if (st != RQ_OK) return st;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->gparts) HIP_TRY(hipFree(ctx->gparts));
+    ctx->gparts = nullptr;
+    ctx->gparts_cap = 0;
+    HIP_TRY(hipMalloc((void**)&ctx->gparts, (size_t)values * 4));
+    ctx->gparts_cap = values;
+    return RQ_OK;
+}
+
+// k-slices of the route's product out[m][rows] = x[m][k] W[rows][k]^T
+// (RQ_GEMM_SPLITS forces a count). Only long rows are split: with k >= 8192
+// the output's 256 x 128 blocks are too few to fill the GPU (ffn_down
+// 4096 x 14336 at m = 128: 16 blocks), so each slice adds as many blocks
+// again, up to 256 blocks and 8 slices of at least 1792 values (there:
+// 79.5 -> 43.0 us at m = 128, 113 -> 90 us at m = 512). At k = 4096
+// splitting measured slower (14336 x 4096 at m = 64: 30.4 -> 38.6 us with 2
+// slices). Each slice is a multiple of 64 values.
+int gemm_splits(const rq_ctx* ctx, int64_t rows, int64_t m, int64_t k) {
+    int S = 1;
+    if (ctx->gemm_splits > 0) {
+        S = ctx->gemm_splits;
+    } else if (k >= 8192) {
+        const int64_t blocks = ((rows + 255) / 256) * ((m + 127) / 128);
+        S = (int)std::max<int64_t>(1, std::min<int64_t>(kMaxGemmSplits, 256 / blocks));
+        while (S > 1 && k / S < 1792) S--;
+    }
+    while (S > 1 && k % (64 * S) != 0) S--;
+    return S;
+}
+
 // The weight's elements as f16 [rows][cols] at out, from whichever layout it
 // holds (the dot4 one when both).
 rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out) {
@@ -1919,13 +1967,35 @@ rq_status gemm_route(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* co
         }
         // Row-major out[m][rows] is the column-major rows x m product
         // W (column-major k x rows, transposed) times x (column-major k x m).
-        bs = rocblas_gemm_ex(ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)w->rows,
-                             (rocblas_int)m, (rocblas_int)k, &alpha, a, rocblas_datatype_f16_r, (rocblas_int)k,
-                             ctx->x16, rocblas_datatype_f16_r, (rocblas_int)k, &beta, outs[i], rocblas_datatype_f32_r,
-                             (rocblas_int)w->rows, outs[i], rocblas_datatype_f32_r, (rocblas_int)w->rows,
-                             rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        const int S = gemm_splits(ctx, w->rows, m, k);
+        if (S == 1) {
+            bs = rocblas_gemm_ex(ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)w->rows,
+                                 (rocblas_int)m, (rocblas_int)k, &alpha, a, rocblas_datatype_f16_r, (rocblas_int)k,
+                                 ctx->x16, rocblas_datatype_f16_r, (rocblas_int)k, &beta, outs[i],
+                                 rocblas_datatype_f32_r, (rocblas_int)w->rows, outs[i], rocblas_datatype_f32_r,
+                                 (rocblas_int)w->rows, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+            if (bs != rocblas_status_success)
+                return fail(RQ_ERR_BACKEND, "rocblas_gemm_ex: %s (%d)", rocblas_status_to_string(bs), (int)bs);
+            continue;
+        }
+        // Split k: slice s of both operands starts s k/S values into each
+        // column; its product goes to parts + s ns, and rq_sum_parts adds
+        // the slices in order (no atomics: the same bits every run).
+        const int64_t n = w->rows * m, ns = (n + 3) & ~int64_t(3), kS = k / S;
+        if ((st = grow_parts(ctx, S * ns)) != RQ_OK) return st;
+        bs = rocblas_gemm_strided_batched_ex(
+            ctx->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)w->rows, (rocblas_int)m,
+            (rocblas_int)kS, &alpha, a, rocblas_datatype_f16_r, (rocblas_int)k, (rocblas_stride)kS, ctx->x16,
+            rocblas_datatype_f16_r, (rocblas_int)k, (rocblas_stride)kS, &beta, ctx->gparts, rocblas_datatype_f32_r,
+            (rocblas_int)w->rows, (rocblas_stride)ns, ctx->gparts, rocblas_datatype_f32_r, (rocblas_int)w->rows,
+            (rocblas_stride)ns, S, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
         if (bs != rocblas_status_success)
-            return fail(RQ_ERR_BACKEND, "rocblas_gemm_ex: %s (%d)", rocblas_status_to_string(bs), (int)bs);
+            return fail(RQ_ERR_BACKEND, "rocblas_gemm_strided_batched_ex: %s (%d)", rocblas_status_to_string(bs),
+                        (int)bs);
+        RqSumParams sp{ctx->gparts, outs[i], n, ns, S, 0};
+        if ((st = launch(ctx, ctx->sum_parts, "rq_sum_parts", (uint64_t)((n / 4 + RQ_THREADS) / RQ_THREADS), &sp)) !=
+            RQ_OK)
+            return st;
     }
     return RQ_OK;
 }

@@ -1444,6 +1444,24 @@ RQ_DEQUANT16(q8_0, RQ_FMT_Q8_0)
 RQ_DEQUANT16(q4_k, RQ_FMT_Q4_K)
 RQ_DEQUANT16(q6_k, RQ_FMT_Q6_K)
 
+// The split-k GEMM's partial products summed in slice order (the same bits
+// every run), four values per thread; out is only 4-byte aligned.
+extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_sum_parts(RqSumParams p) {
+    const int64_t i = ((int64_t)blockIdx.x * RQ_THREADS + threadIdx.x) * 4;
+    if (i >= p.n) return;
+    const int4 a = ld16(p.parts + i);
+    float v[4] = {__int_as_float(a.x), __int_as_float(a.y), __int_as_float(a.z), __int_as_float(a.w)};
+    for (int s = 1; s < p.S; s++) {
+        const int4 b = ld16(p.parts + s * p.ns + i);
+        v[0] += __int_as_float(b.x);
+        v[1] += __int_as_float(b.y);
+        v[2] += __int_as_float(b.z);
+        v[3] += __int_as_float(b.w);
+    }
+    const int e = p.n - i < 4 ? (int)(p.n - i) : 4;
+    for (int j = 0; j < e; j++) gmem(p.out)[i + j] = v[j];
+}
+
 // Eight values per thread.
 extern "C" __global__ __launch_bounds__(RQ_THREADS) void rq_f32_to_f16(RqConvParams p) {
     const int64_t i = ((int64_t)blockIdx.x * RQ_THREADS + threadIdx.x) * 8;

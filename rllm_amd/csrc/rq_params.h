@@ -296,6 +296,16 @@ struct RqDequantParams {
 };
 
 // f32 -> f16 (round to nearest even) of n values, n % 8 == 0 (rq_f32_to_f16).
+// The f16 GEMM route's split-k sum: out[i] = parts[0][i] + ... + parts[S-1][i]
+// (in that order), i < n, parts[s] = parts + s * ns (ns: n rounded up to a
+// multiple of 4; parts 16-byte aligned).
+struct RqSumParams {
+    const float* parts;
+    float* out;
+    int64_t n, ns;
+    int32_t S, pad;
+};
+
 struct RqConvParams {
     const float* x;
     uint16_t* y;
