@@ -253,6 +253,55 @@ def bench_floor(torch, gpu, t, n, k, steps, warmup):
     return {"us": statistics.median(per_launch), "spread": spread(per_launch), "bytes": nbytes}
 
 
+# (kind, threads, workgroups) of the read-floor shapes for Q4_K 14336x4096's
+# 3,584 tiles (rq_floor_shape): one tile per wave in 256 / 512 / 1024-thread
+# workgroups, two tiles per wave, and grid-stride waves over 256-1024
+# workgroups.
+FLOOR_SHAPES = [(1, 256, 896), (1, 512, 448), (1, 1024, 224), (2, 256, 448), (2, 512, 224), (2, 1024, 112),
+                (3, 256, 256), (3, 256, 512), (3, 512, 256), (3, 1024, 256), (3, 256, 1024), (3, 512, 512)]
+
+
+def floor_shapes(argv) -> int:
+    """bench.py --floor-shapes [STEPS]: the headline's 33 MB read (3,584
+    tiles of 9 KiB, rotating copies) in each launch shape of FLOOR_SHAPES,
+    timed as bench_matvec (graph replays of 252 launches). One JSON line per
+    shape: what the memory traffic alone costs a launch of that shape."""
+    import torch
+
+    from rllm_amd import build as rq_build
+    from rllm_amd.backend import HipBackend
+
+    steps = int(argv[0]) if argv else 10
+    L = ctypes.CDLL(rq_build.FLOOR_LIB)
+    L.rq_floor_shape.restype = ctypes.c_int
+    L.rq_floor_shape.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
+                                 ctypes.c_void_p, ctypes.c_void_p]
+    gpu = HipBackend(0)
+    tiles = 3584
+    nbytes = tiles * 9 * 1024
+    copies = rotation_copies(nbytes)
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=gpu.device) for _ in range(copies)]
+    out = torch.empty(tiles * 4, dtype=torch.int32, device=gpu.device)
+    chunk = max(1, 256 // copies) * copies
+    for kind, threads, grid in FLOOR_SHAPES:
+        def launch(i, kind=kind, threads=threads, grid=grid):
+            rc = L.rq_floor_shape(kind, bufs[i % copies].data_ptr(), tiles, threads, grid, out.data_ptr(),
+                                  gpu.stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"rq_floor_shape: hipError {rc}")
+
+        per, g = time_graph(torch, gpu, launch, chunk, steps, 2)
+        assert int(out[0].item()) == 0  # all-ones input: the XOR fold of an even word count
+        del g
+        per_launch = [p / chunk for p in per]
+        us = statistics.median(per_launch)
+        print(json.dumps({"kind": kind, "threads": threads, "workgroups": grid, "us": round(us, 3),
+                          "spread_us": spread(per_launch), "GB_s": round(nbytes / us / 1e3, 1)}), flush=True)
+    del bufs
+    gpu.close()
+    return 0
+
+
 class FloorTarget(ctypes.Structure):
     """RqFloorTarget of rq_floor.hip."""
     _fields_ = [("base", ctypes.c_void_p), ("tail", ctypes.c_void_p), ("tiles", ctypes.c_int64),
@@ -956,6 +1005,8 @@ def main() -> int:
         return timeline(sys.argv[sys.argv.index("--timeline") + 1:])
     if "--matmul-routes" in sys.argv:
         return matmul_routes(sys.argv[sys.argv.index("--matmul-routes") + 1:])
+    if "--floor-shapes" in sys.argv:
+        return floor_shapes(sys.argv[sys.argv.index("--floor-shapes") + 1:])
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20, help="timed graph replays (steps) of the headline matvec")

@@ -248,6 +248,81 @@ extern "C" int rq_floor_read_many(const void* targets, int count, int pair, int 
     return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Other launch shapes of the same read (rq_floor_read's tiles of C = 9
+// chunks, 16-byte nontemporal loads contiguous across a wave, XOR fold, one
+// word per 16 lanes): does any shape read the bytes faster?
+//   kind 1: one tile per wave, `threads` per workgroup;
+//   kind 2: two consecutive tiles per wave, all 18 loads issued first;
+//   kind 3: grid-stride, wave w reads tiles w, w + W, ... (W waves in all).
+template <int TPW>
+__global__ __launch_bounds__(1024) void rq_floor_shape_k(const u8* __restrict__ base, int64_t tiles,
+                                                         u32* __restrict__ out) {
+    constexpr int C = 9;
+    const int lane = threadIdx.x & 63;
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    int4 v[TPW][C];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int64_t t = w * TPW + j;
+#pragma unroll
+        for (int c = 0; c < C; c++) v[j][c] = t < tiles ? ld16_nt(base + ((t * C + c) * 64 + lane) * 16) : make_int4(0, 0, 0, 0);
+    }
+    int x = 0;
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+#pragma unroll
+        for (int c = 0; c < C; c++) x ^= v[j][c].x ^ v[j][c].y ^ v[j][c].z ^ v[j][c].w;
+    x ^= dpp_i<DPP_QUAD_1032>(x);
+    x ^= dpp_i<DPP_QUAD_2301>(x);
+    x ^= dpp_i<DPP_ROW_HALF_MIRROR>(x);
+    x ^= dpp_i<DPP_ROW_MIRROR>(x);
+    if (w * TPW < tiles && (lane & 15) == 0) out[w * 4 + (lane >> 4)] = (u32)x;
+}
+
+__global__ __launch_bounds__(1024) void rq_floor_stride_k(const u8* __restrict__ base, int64_t tiles,
+                                                          u32* __restrict__ out) {
+    constexpr int C = 9;
+    const int lane = threadIdx.x & 63;
+    const int64_t W = (int64_t)gridDim.x * (blockDim.x >> 6);
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    int x = 0;
+    for (int64_t t = w; t < tiles; t += W) {
+        int4 v[C];
+#pragma unroll
+        for (int c = 0; c < C; c++) v[c] = ld16_nt(base + ((t * C + c) * 64 + lane) * 16);
+#pragma unroll
+        for (int c = 0; c < C; c++) x ^= v[c].x ^ v[c].y ^ v[c].z ^ v[c].w;
+    }
+    x ^= dpp_i<DPP_QUAD_1032>(x);
+    x ^= dpp_i<DPP_QUAD_2301>(x);
+    x ^= dpp_i<DPP_ROW_HALF_MIRROR>(x);
+    x ^= dpp_i<DPP_ROW_MIRROR>(x);
+    if (w < tiles && (lane & 15) == 0) out[w * 4 + (lane >> 4)] = (u32)x;
+}
+
+// Launches shape `kind` over `tiles` tiles of 9 KiB at `base` (16-byte
+// aligned) in `grid` workgroups of `threads` (64 .. 1024, a multiple of 64);
+// out holds 4 x tiles words. Kinds 1 and 2 need grid x threads / 64 x kind
+// >= tiles. Returns a hipError_t.
+extern "C" int rq_floor_shape(int kind, const void* base, int64_t tiles, int threads, int64_t grid, void* out,
+                              void* stream) {
+    if (!base || !out || tiles <= 0 || threads < 64 || threads > 1024 || threads % 64 != 0 || grid <= 0 ||
+        grid > 0x7fffffff || ((uintptr_t)base & 15) != 0)
+        return (int)hipErrorInvalidValue;
+    const int64_t waves = grid * (threads / 64);
+    if ((kind == 1 || kind == 2) && waves * kind < tiles) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const u8* b = (const u8*)base;
+    switch (kind) {
+    case 1: hipLaunchKernelGGL(rq_floor_shape_k<1>, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
+    case 2: hipLaunchKernelGGL(rq_floor_shape_k<2>, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
+    case 3: hipLaunchKernelGGL(rq_floor_stride_k, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
+    default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void rq_floor_empty_k() {}
 
 // Launches `workgroups` empty 256-thread workgroups on `stream`. Returns a
