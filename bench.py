@@ -255,10 +255,11 @@ def bench_floor(torch, gpu, t, n, k, steps, warmup):
 
 # (kind, threads, workgroups) of the read-floor shapes for Q4_K 14336x4096's
 # 3,584 tiles (rq_floor_shape): one tile per wave in 256 / 512 / 1024-thread
-# workgroups, two tiles per wave, and grid-stride waves over 256-1024
-# workgroups.
+# workgroups, two tiles per wave, grid-stride waves over 256-1024
+# workgroups, and one tile per wave with each XCD on a contiguous eighth.
 FLOOR_SHAPES = [(1, 256, 896), (1, 512, 448), (1, 1024, 224), (2, 256, 448), (2, 512, 224), (2, 1024, 112),
-                (3, 256, 256), (3, 256, 512), (3, 512, 256), (3, 1024, 256), (3, 256, 1024), (3, 512, 512)]
+                (3, 256, 256), (3, 256, 512), (3, 512, 256), (3, 1024, 256), (3, 256, 1024), (3, 512, 512),
+                (4, 256, 896), (4, 512, 448)]
 
 
 def floor_shapes(argv) -> int:

@@ -254,13 +254,18 @@ extern "C" int rq_floor_read_many(const void* targets, int count, int pair, int 
 // word per 16 lanes): does any shape read the bytes faster?
 //   kind 1: one tile per wave, `threads` per workgroup;
 //   kind 2: two consecutive tiles per wave, all 18 loads issued first;
-//   kind 3: grid-stride, wave w reads tiles w, w + W, ... (W waves in all).
-template <int TPW>
+//   kind 3: grid-stride, wave w reads tiles w, w + W, ... (W waves in all);
+//   kind 4: kind 1 with each XCD's workgroups on one contiguous eighth.
+template <int TPW, bool XCD = false>
 __global__ __launch_bounds__(1024) void rq_floor_shape_k(const u8* __restrict__ base, int64_t tiles,
                                                          u32* __restrict__ out) {
     constexpr int C = 9;
     const int lane = threadIdx.x & 63;
-    const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // XCD: workgroup b runs on XCD b % 8 (round-robin dispatch); it takes
+    // workgroup slot (b % 8) * (G / 8) + b / 8, so that each XCD reads one
+    // contiguous eighth of the buffer (G a multiple of 8).
+    const int64_t bx = XCD ? (int64_t)(blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int64_t w = bx * (blockDim.x >> 6) + (threadIdx.x >> 6);
     int4 v[TPW][C];
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
@@ -311,13 +316,15 @@ extern "C" int rq_floor_shape(int kind, const void* base, int64_t tiles, int thr
         grid > 0x7fffffff || ((uintptr_t)base & 15) != 0)
         return (int)hipErrorInvalidValue;
     const int64_t waves = grid * (threads / 64);
-    if ((kind == 1 || kind == 2) && waves * kind < tiles) return (int)hipErrorInvalidValue;
+    if ((kind == 1 || kind == 2 || kind == 4) && waves * (kind == 2 ? 2 : 1) < tiles) return (int)hipErrorInvalidValue;
+    if (kind == 4 && grid % 8 != 0) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const u8* b = (const u8*)base;
     switch (kind) {
     case 1: hipLaunchKernelGGL(rq_floor_shape_k<1>, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
     case 2: hipLaunchKernelGGL(rq_floor_shape_k<2>, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
     case 3: hipLaunchKernelGGL(rq_floor_stride_k, dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
+    case 4: hipLaunchKernelGGL((rq_floor_shape_k<1, true>), dim3((unsigned)grid), dim3(threads), 0, s, b, tiles, (u32*)out); break;
     default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
