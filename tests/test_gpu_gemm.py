@@ -174,6 +174,28 @@ def test_keep_f16_gives_the_same_bits(route, orc):
         wg.free()
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_keep_f16_lifecycle(gpu, orc):
+    """rq_weight_keep_f16 allocates, so a capturing stream refuses it; the
+    copy's rows * cols * 2 bytes of device memory go back with the weight."""
+    n, k = 4096, 4096
+    w = make_weight(orc, 12, n, k, 77, "normal")
+    wg = upload(gpu, 12, w, n, k)
+    torch.cuda.synchronize()
+    with pytest.raises(ShapeError, match="rq_weight_keep_f16"):
+        _capture(gpu, lambda: gpu.keep_f16(wg))
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(gpu.device)
+    gpu.keep_f16(wg)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info(gpu.device)
+    assert free0 - free1 >= n * k * 2, f"keep_f16 took {free0 - free1} bytes"
+    wg.free()
+    torch.cuda.synchronize()
+    free2, _ = torch.cuda.mem_get_info(gpu.device)
+    assert free2 - free1 >= n * k * 2, f"freeing the weight returned {free2 - free1} bytes"
+
+
 def test_below_min_m_keeps_the_int8_path(gpu, orc):
     """Under the threshold (and for rq_matmul_many_noalloc at any m) results
     are the int8 path's, bit for bit."""
