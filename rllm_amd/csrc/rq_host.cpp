@@ -281,6 +281,10 @@ struct rq_ctx {
     hipFunction_t sum_parts = nullptr;
     float* gparts = nullptr;
     int64_t gparts_cap = 0;
+    // The gated FFN's up product on the route when the caller gives no up
+    // buffer (f32, m * n_ffn values).
+    float* uroute = nullptr;
+    int64_t uroute_cap = 0;
     int gemm_splits = 0;
     int kernels = RQ_KERNELS_AUTO;  // family later uploads are laid out for
     int mmq_sbw = 0, mmq_tr = 0;    // tuning overrides (RQ_MMQ_SBW, RQ_MMQ_TR; 0 = planned)
@@ -1364,6 +1368,7 @@ extern "C" rq_status rq_close(rq_ctx* ctx) {
         if (ctx->w16) (void)hipFree(ctx->w16);
         if (ctx->x16) (void)hipFree(ctx->x16);
         if (ctx->gparts) (void)hipFree(ctx->gparts);
+        if (ctx->uroute) (void)hipFree(ctx->uroute);
         if (ctx->up_stream) (void)hipStreamSynchronize(ctx->up_stream);
         for (int b = 0; b < 2; b++) {
             if (ctx->up_pin[b]) (void)hipHostFree(ctx->up_pin[b]);
@@ -1763,6 +1768,7 @@ rq_status grow_f16(rq_ctx* ctx, uint16_t** p, int64_t* cap, int64_t values);
 rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out);
 rq_status refuse_capture(rq_ctx* ctx, const char* what);
 rq_status grow_parts(rq_ctx* ctx, int64_t values);
+rq_status grow_uroute(rq_ctx* ctx, int64_t values);
 }  // namespace
 
 extern "C" rq_status rq_set_gemm_min_m(rq_ctx* ctx, int64_t m) {
@@ -1782,7 +1788,8 @@ extern "C" rq_status rq_reserve_f16(rq_ctx* ctx, int64_t weight_values, int64_t 
     if ((st = ensure_blas(ctx)) != RQ_OK) return st;
     if ((st = grow_f16(ctx, &ctx->w16, &ctx->w16_cap, weight_values)) != RQ_OK) return st;
     if ((st = grow_f16(ctx, &ctx->x16, &ctx->x16_cap, x_values)) != RQ_OK) return st;
-    return grow_parts(ctx, kMaxGemmSplits * ((out_values + 3) & ~int64_t(3)));
+    if ((st = grow_parts(ctx, kMaxGemmSplits * ((out_values + 3) & ~int64_t(3)))) != RQ_OK) return st;
+    return grow_uroute(ctx, out_values);
 }
 
 extern "C" rq_status rq_weight_keep_f16(rq_ctx* ctx, rq_weight* w) {
@@ -1894,6 +1901,19 @@ rq_status grow_parts(rq_ctx* ctx, int64_t values) {
     return RQ_OK;
 }
 
+rq_status grow_uroute(rq_ctx* ctx, int64_t values) {
+    if (values <= ctx->uroute_cap) return RQ_OK;
+    rq_status st = refuse_capture(ctx, "gated FFN up scratch too small");
+    if (st != RQ_OK) return st;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->uroute) HIP_TRY(hipFree(ctx->uroute));
+    ctx->uroute = nullptr;
+    ctx->uroute_cap = 0;
+    HIP_TRY(hipMalloc((void**)&ctx->uroute, (size_t)values * 4));
+    ctx->uroute_cap = values;
+    return RQ_OK;
+}
+
 // k-slices of the route's product out[m][rows] = x[m][k] W[rows][k]^T
 // (RQ_GEMM_SPLITS forces a count). Only long rows are split: with k >= 8192
 // the output's 256 x 128 blocks are too few to fill the GPU (ffn_down
@@ -1940,6 +1960,9 @@ rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out) {
     const int64_t grid = w->dot4 ? (w->rows * U + RQ_THREADS - 1) / RQ_THREADS : (int64_t)w->tiles * ((U + 15) / 16);
     return launch(ctx, f, "rq_dequant16", (uint64_t)grid, &p);
 }
+
+// Whether batched matmuls of m columns take the f16 GEMM route.
+bool gemm_route_takes(const rq_ctx* ctx, int64_t m) { return ctx->gemm_min_m > 0 && m >= ctx->gemm_min_m; }
 
 rq_status gemm_route(rq_ctx* ctx, const float* x, int64_t m, const rq_weight* const* ws, float* const* outs,
                      int count) {
@@ -2038,7 +2061,7 @@ rq_status matmul_many_run(rq_ctx* ctx, const float* x, int64_t x_len, int64_t m,
     // Prefill-size batches (m >= rq_set_gemm_min_m's value, 65 unless set):
     // the f16 GEMM route. Never for rq_matmul_many_noalloc, whose point is
     // to allocate nothing.
-    if (!fixed && ctx->gemm_min_m > 0 && m >= ctx->gemm_min_m) return gemm_route(ctx, x, m, ws, outs, count);
+    if (!fixed && gemm_route_takes(ctx, m)) return gemm_route(ctx, x, m, ws, outs, count);
     // m == 1: each launch quantizes x while staging it (bit-identical to
     // rq_quantize_q8_1), saving the quantize launch. For m >= 2 the staging
     // of f32 columns costs every workgroup more than the launch saves
@@ -2191,6 +2214,23 @@ rq_status glu_run(rq_ctx* ctx, const float* x, const rq_q8_1* xq, int64_t m, con
                   const rq_weight* up, int act, float* hf, float* u_buf, int8_t* hq, uint16_t* hd, uint16_t* hs) {
     const int64_t k = gate->cols, n = gate->rows;
     rq_status st;
+    if (!xq && gemm_route_takes(ctx, m)) {
+        // Prefill-size m over f32 x: the reference's m > 8 route on gfx950,
+        // where no int8 tile kernel runs the down projection (gated_ffn,
+        // backend.rs:1690-1692, 1731-1743): gate and up through the f16
+        // GEMM route, then the elementwise activation (and the Q8_1 of h
+        // when asked for).
+        float* ub = u_buf;
+        if (!ub) {
+            if ((st = grow_uroute(ctx, m * n)) != RQ_OK) return st;
+            ub = ctx->uroute;
+        }
+        const rq_weight* ws[2] = {gate, up};
+        float* outs[2] = {hf, ub};
+        const int64_t lens[2] = {m * n, m * n};
+        if ((st = rq_matmul_many(ctx, x, m * k, m, ws, outs, lens, 2)) != RQ_OK) return st;
+        return act_mul_launch(ctx, act, hf, ub, m * n, hq, hd, hs);
+    }
     if (glu_mmq_ok(gate, up, m)) {
         if (xq) return mmq_glu_launch(ctx, xq->qs, xq->d, nullptr, m, gate, up, act, hf, hq, hd, hs);
         if (m == 1) return mmq_glu_launch(ctx, nullptr, nullptr, x, 1, gate, up, act, hf, hq, hd, hs);
@@ -2335,6 +2375,13 @@ extern "C" rq_status rq_glu_matmul(rq_ctx* ctx, const float* x, int64_t x_len, i
         if (!up_scratch || !aligned(up_scratch, 16))
             return fail(RQ_ERR_INVALID, "glu_matmul: up scratch must be a 16-byte aligned pointer");
     }
+    // The f16 GEMM route writes up's product to the up scratch when one is
+    // given (else to the context's).
+    if (gemm_route_takes(ctx, m) && up_scratch) {
+        if ((st = check_len("glu_matmul up", up_len, m * n)) != RQ_OK) return st;
+        if (!aligned(up_scratch, 16))
+            return fail(RQ_ERR_INVALID, "glu_matmul: up scratch must be a 16-byte aligned pointer");
+    }
     if ((st = bind(ctx)) != RQ_OK) return st;
     return glu_run(ctx, x, nullptr, m, gate, up, act, out, up_scratch, nullptr, nullptr, nullptr);
 }
@@ -2360,10 +2407,20 @@ rq_status gated_ffn_run(rq_ctx* ctx, const char* what, const float* x, int64_t x
     if (!glu_fusable(gate, up, m) && !glu_mmq_ok(gate, up, m) &&
         (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK)
         return st;
+    // The f16 GEMM route (f32 x) writes up's product to up_buf when given.
+    if (!xq && gemm_route_takes(ctx, m) && up_buf && (st = check_len("gated_ffn up", up_len, m * n)) != RQ_OK)
+        return st;
     if (m == 0) return RQ_OK;
     if (!out || !gate_buf || !aligned(out, 4) || !aligned(gate_buf, 16) || (up_buf && !aligned(up_buf, 16)))
         return fail(RQ_ERR_INVALID, "%s: null or misaligned buffer", what);
     if ((st = bind(ctx)) != RQ_OK) return st;
+    // Prefill-size m over f32 x: h in f32 (gate_buf), then down through the
+    // f16 GEMM route as well.
+    if (!xq && gemm_route_takes(ctx, m)) {
+        if ((st = glu_run(ctx, x, nullptr, m, gate, up, act, gate_buf, up_buf, nullptr, nullptr, nullptr)) != RQ_OK)
+            return st;
+        return rq_matmul(ctx, gate_buf, m * n, m, down, out, m * down->rows);
+    }
     // The product goes to the down projection as Q8_1, written by the launch
     // that computes it (as the reference's glu_mmq int8 copy, backend.rs:989-1093).
     if ((st = ensure_hscratch(ctx, m * n)) != RQ_OK) return st;
