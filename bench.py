@@ -434,11 +434,14 @@ def bench_qkv(torch, gpu, orc, steps, warmup):
     return {"us": us, "spread": spread(per_launch), "gbs": b / us / 1e3, "bytes": b}
 
 
-def bench_ffn(torch, gpu, orc, steps, warmup, m=1):
+def bench_ffn(torch, gpu, orc, steps, warmup, m=1, family=None, min_m=None):
     """BASELINE config 3 as the decode step runs it: gated_ffn (gate/up
     Q4_K 14336 x 4096 fused with SiLU and the product's Q8_1, down Q6_K
-    4096 x 14336) over rotating copies. Returns dict(us, spread, gbs)."""
-    from rllm_amd.backend import Activation
+    4096 x 14336) over rotating copies of `family` weights (None: the
+    library's default layout). min_m: rq_set_gemm_min_m for the call (the
+    f16 GEMM route from that many columns; 0: never). Returns dict(us,
+    spread, gbs)."""
+    from rllm_amd.backend import GEMM_MIN_M_DEFAULT, Activation
 
     f, d = 14336, 4096
     g_w = make_gguf(orc, 12, f, d, 31)
@@ -446,14 +449,20 @@ def bench_ffn(torch, gpu, orc, steps, warmup, m=1):
     d_w = make_gguf(orc, 14, d, f, 33)
     per_set = g_w.nbytes + u_w.nbytes + d_w.nbytes
     copies = rotation_copies(per_set)
-    sets = [(upload_copies(gpu, 12, f, d, g_w, 1)[0], upload_copies(gpu, 12, f, d, u_w, 1)[0],
-             upload_copies(gpu, 14, d, f, d_w, 1)[0]) for _ in range(copies)]
+    sets = [(upload_copies(gpu, 12, f, d, g_w, 1, family)[0], upload_copies(gpu, 12, f, d, u_w, 1, family)[0],
+             upload_copies(gpu, 14, d, f, d_w, 1, family)[0]) for _ in range(copies)]
     x = gpu.from_host(orc.normal(34, m * d))
     out, gb, ub = gpu.alloc(m * d), gpu.alloc(m * f), gpu.alloc(m * f)
     gpu.reserve(m * f)
+    if min_m is not None:
+        gpu.reserve_f16(f * d, m * f, m * f)
+        gpu.set_gemm_min_m(min_m)
     chunk = max(1, 128 // copies) * copies
-    per, g = time_graph(torch, gpu, lambda i: gpu.gated_ffn(x, *sets[i % copies], Activation.SILU, out, gb, ub, m),
-                        chunk, steps, warmup)
+    try:
+        per, g = time_graph(torch, gpu, lambda i: gpu.gated_ffn(x, *sets[i % copies], Activation.SILU, out, gb, ub, m),
+                            chunk, steps, warmup)
+    finally:
+        gpu.set_gemm_min_m(GEMM_MIN_M_DEFAULT)
     del g
     for s_ in sets:
         for w in s_:
@@ -1179,6 +1188,17 @@ def main() -> int:
                                     "pct_mfma_peak": round(100 * tf / (INT8_MFMA_PEAK_TOPS if route == "int8"
                                                                         else F16_MFMA_PEAK_TFLOPS), 2),
                                     "check_rel": v["check_rel"]})
+        # The gated FFN at prompt sizes over f32 x, MFMA weights: the f16
+        # GEMM route (gate/up, act_mul, down; the reference's m > 8 route on
+        # gfx950, backend.rs:1690-1692, 1731-1743) against the int8 path
+        # (fused gate/up in launches of 32 columns, down over h's Q8_1).
+        for m in (128, 512):
+            for route, mm in (("f16 gemm", 1), ("int8", 0)):
+                c = bench_ffn(torch, gpu, orc, 3, 1, m, "mfma", mm)
+                log(f"prefill gated FFN 14336/4096 m={m} ({route}): {c['us']:.1f} us")
+                configs.append({"config": "prefill gated FFN (gate/up Q4_K 14336x4096 + SiLU, down Q6_K 4096x14336)",
+                                "route": route, "kernels": "mfma", "batch": m, "us": round(c["us"], 2),
+                                "spread_us": c["spread"], "tokens_per_s": round(m / c["us"] * 1e6, 1)})
         # One GPU's share at tensor-parallel degree 8 (row slices of gate and
         # the head, a k slice of down): the kernels at their real shard shapes.
         plan += [("TP8 shard", 12, 1792, 4096, 1, None), ("TP8 shard", 14, 4096, 1792, 1, None),
