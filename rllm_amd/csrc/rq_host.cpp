@@ -1957,10 +1957,11 @@ rq_status dequant16_launch(rq_ctx* ctx, const rq_weight* w, uint16_t* out) {
     // One thread per (row, 32-element block): the dot4 layout's blocks in
     // row order, the MFMA layout's as workgroups of 16 blocks of one tile.
     const int64_t U = w->cols / 32;
-    // (Q6_K in the dot4 layout: workgroups of 64 (row, super-block) pairs.)
-    const int64_t grid = !w->dot4                ? (int64_t)w->tiles * ((U + 15) / 16)
-                         : w->fmt == RQ_FMT_Q6_K ? (w->rows * w->tiled.S + 63) / 64
-                                                 : (w->rows * U + RQ_THREADS - 1) / RQ_THREADS;
+    // Q6_K: workgroups of 64 (row, super-block) pairs in the dot4 layout, of
+    // 4 super-blocks of one tile in the MFMA layout.
+    const bool q6 = w->fmt == RQ_FMT_Q6_K;
+    const int64_t grid = w->dot4 ? (q6 ? (w->rows * w->tiled.S + 63) / 64 : (w->rows * U + RQ_THREADS - 1) / RQ_THREADS)
+                                 : (int64_t)w->tiles * (q6 ? (w->cols / 256 + 3) / 4 : (U + 15) / 16);
     return launch(ctx, f, "rq_dequant16", (uint64_t)grid, &p);
 }
 
