@@ -1037,7 +1037,8 @@ def main() -> int:
     os.environ["RQ_KERNELS"] = args.kernels  # read by rq_open, here and in the traffic child
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the matvec path has no "
-              "multi-GPU code; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "multi-GPU code: row-parallel weights would shard by output rows, column-parallel ones by k "
+              "with one all-reduce per layer)", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
