@@ -1086,6 +1086,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     constexpr int FMT = RQ_FMT_Q6_K;
     constexpr int NLD = 3 * SBW;               // code loads per lane
     constexpr int NACC = MP == 8 ? 2 : 1;
+    static_assert(SBW == 2 || SBW == 4 || SBW == 8, "Q6_K: the d load takes 2, 4 or 8 super-blocks");
     constexpr int NA = MP == 1 ? 4 : (MP == 4 ? 1 : 2);  // A register sets (phases)
 
     const int tid = threadIdx.x;
@@ -1132,12 +1133,18 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     auto load_w = [&]() {
         const int DS = (S2 + 7) & ~7;
         const u8* dp = T.hdr + (int64_t)T.tiles * S2 * 256 + ((int64_t)(tile_c * 16 + n) * DS + sb0) * 2;
-        if (SBW == 2) {
+        if constexpr (SBW == 2) {
             dw[0] = ld4_nt(dp);
-        } else if (SBW == 4) {
+        } else if constexpr (SBW == 4) {
             const uint2 v = ld8_nt(dp);
             dw[0] = v.x;
-            dw[SBW / 2 - 1] = v.y;
+            dw[1] = v.y;
+        } else {  // 8: sb0 is a multiple of 8, so 16-byte aligned
+            const int4 v = ld16_nt(dp);
+            dw[0] = (u32)v.x;
+            dw[1] = (u32)v.y;
+            dw[2] = (u32)v.z;
+            dw[3] = (u32)v.w;
         }
         const int nvalid = nsb * 3;
         const u8* cb = T.code + ((int64_t)tile_c * 3 * S2 + (int64_t)sb0 * 3) * 1024 + lane * 16;
@@ -1307,6 +1314,7 @@ template <int SBW, int G, bool GLU>
 __device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
     constexpr int FMT = RQ_FMT_Q6_K;
     constexpr int NLD = 3 * SBW;  // code loads per lane
+    static_assert(SBW == 2 || SBW == 4, "Q6_K 16-column groups: the d load takes 2 or 4 super-blocks");
 
     const int tid = threadIdx.x, threads = blockDim.x;
     const int lane = tid & 63;
@@ -1495,8 +1503,14 @@ RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 8, 4)
     extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_8x4(RqMmqParams p) {       \
         mmq_run<FMT, 8, 4, false, false, 4, true>(p);                                                \
     }                                                                                                \
+    extern "C" __global__ __launch_bounds__(512) void rq_mmqglu_##NAME##_1s8(RqMmqParams p) {        \
+        mmq_run<FMT, 1, 8, false, false, 1, true>(p);                                                \
+    }                                                                                                \
     extern "C" __global__ __launch_bounds__(1024) void rq_mmqgluf_##NAME(RqMmqParams p) {            \
         mmq_run<FMT, 1, 4, true, false, 1, true>(p);                                                 \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(512) void rq_mmqgluf_##NAME##_s8(RqMmqParams p) {        \
+        mmq_run<FMT, 1, 8, true, false, 1, true>(p);                                                 \
     }
 RQ_MMQ_GLU_SET(q4_0, RQ_FMT_Q4_0)
 RQ_MMQ_GLU_SET(q8_0, RQ_FMT_Q8_0)

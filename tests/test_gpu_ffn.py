@@ -243,6 +243,35 @@ def test_gated_ffn_q8_1_input(gpuk, orc, tname, m):
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
+@pytest.mark.parametrize("d", [2304, 3072, 3328, 4096])
+def test_gated_ffn_one_column_split(gpuk, orc, tname, d):
+    """One column over rows of 9, 12, 13 and 16 super-blocks: the MFMA GLU's
+    8-super-block k-parts (a last part of 2, 4, 6 and 8 of the padded row).
+    h within 1e-3 of the int8 oracle; the f32 and Q8_1 inputs give the same
+    h and output bit for bit."""
+    t, f = TYPES[tname], 512
+    gw = orc.random_weight(0xF0 + d, t, f, d)
+    uw = orc.random_weight(0xF1 + d, t, f, d)
+    dw = orc.random_weight(0xF2 + d, t, d, f)
+    g, u, dn = upload(gpuk, t, gw, f, d), upload(gpuk, t, uw, f, d), upload(gpuk, t, dw, d, f)
+    x = orc.normal(0xF3 + d, d, 0.0, 1.0)
+    xb = gpuk.from_host(x)
+    outs = []
+    for use_q8 in (False, True):
+        out, gb, ub = gpuk.alloc(d), gpuk.alloc(f), gpuk.alloc(f)
+        if use_q8:
+            gpuk.gated_ffn_q8_1(gpuk.quantize_q8_1(xb, 1, d), g, u, dn, Activation.SILU, out, gb, ub, 1)
+        else:
+            gpuk.gated_ffn(xb, g, u, dn, Activation.SILU, out, gb, ub, 1)
+        outs.append((gpuk.to_host(out, d), gpuk.to_host(gb, f)))
+    qs, dq, _ = orc.quantize_q8_1(x, 1, d)
+    want_h = orc.glu_q8_1(t, gw, uw, f, d, qs, dq, 1, int(Activation.SILU))
+    orc.assert_close(f"h {tname} d={d}", want_h, outs[0][1], 1e-3)
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32)), "h"
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32)), "out"
+
+
+@pytest.mark.parametrize("tname", list(TYPES))
 @pytest.mark.parametrize("d", [5120, 8192, 14336, 20480, 32768])
 @pytest.mark.parametrize("m", [1, 3, 8, 12])
 def test_gated_ffn_wide_inputs(gpuk, orc, tname, d, m):
