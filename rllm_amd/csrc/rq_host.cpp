@@ -743,8 +743,18 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
     L.lds = L.part_off + (dots ? 0 : L.ks * L.tr * 64 * (L.mp == 8 ? 2 : 1) * (L.g > 4 ? 1 : L.g) * 4);
 }
 
+// A Q6_K vocabulary head (>= 16384 rows of 9 to 16 super-blocks) at one
+// column: rq_mmq*_q6_k_*8, 8 super-blocks per wave (128256 x 4096: 66.6 ->
+// 63.9 us; 4096 and 14336 rows of 4096 moved by under 2% either way, and
+// 4096 x 14336 by nothing, so they keep the smaller split).
+constexpr int64_t kQ6HeadTiles = 1024;
+bool q6_head(const rq_weight* w, int64_t m) {
+    return w->fmt == RQ_FMT_Q6_K && m == 1 && w->S2 > 8 && w->S2 <= 16 && w->tiles >= kQ6HeadTiles;
+}
+
 // Launch geometry and LDS layout of an rq_mmq launch over weights of S2
-// super-blocks per row and `tiles` tiles in total.
+// super-blocks per row and `tiles` tiles in total (head: q6_head of every
+// target).
 //   sbw: the fewest super-blocks per wave that keep a tile's k-parts within
 //        one workgroup (shorter waves finish sooner after their last weight
 //        load: fastest for 1 to 4 columns at 14336 x 4096); RQ_MMQ_SBW
@@ -762,7 +772,8 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
 // 16.1 / 26.2 us at 4 tiles per workgroup against 11.3 / 16.6 / 27.8 at 2;
 // Q4_K 4096 x 4096 6.3 / 9.5 / 16.0 at 1 against 9.1 / 14.2 / 24.4 at 4;
 // Q6_K 128256 x 4096 74 / 119 / 204 at 2 against 92 / 139 / 230 at 4.
-MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t tiles, bool f32_in, bool dots) {
+MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t tiles, bool f32_in, bool dots,
+                 bool head) {
     MmqPlan L = cls;
     const int mp = L.mp;
     const int maxs = mmq_sbw_max(fmt);
@@ -775,6 +786,13 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
     if (mp == 16) sbw = mmqt_sbw(fmt, S2, tiles);
     L.np = mmq_np(fmt, S2);
     if (L.np > 1) sbw = 4;  // the wide kernels: 16 k-parts of 4 per tile, in passes
+    // Q6_K heads at one column (q6_head): 8 super-blocks per wave in
+    // 512-thread workgroups (rq_mmq*_q6_k_*8). RQ_MMQ_SBW = 8 takes them for
+    // every one-column Q6_K launch, 2 or 4 never.
+    const bool q6_8 = fmt == RQ_FMT_Q6_K && mp == 1 && L.g == 1 && !dots && L.np == 1 &&
+                      (ctx->mmq_sbw ? ctx->mmq_sbw == 8 : head);
+    if (q6_8) sbw = 8;
+    const int max_waves = q6_8 ? 8 : 16;
     L.sbw = sbw;
     L.ks = L.np > 1 ? 16 : (S2 + sbw - 1) / sbw;
     if (mp == 16 && ctx->mmq_tr == 0) {
@@ -794,7 +812,7 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
         return L;
     }
     if (ctx->mmq_tr > 0 || (mp >= 8 && !dots)) {
-        const int tr_max = std::max(1, 16 / L.ks);
+        const int tr_max = std::max(1, max_waves / L.ks);
         if (ctx->mmq_tr > 0) {
             L.tr = std::min(ctx->mmq_tr, tr_max);
         } else {
@@ -813,7 +831,7 @@ MmqPlan mmq_plan(const rq_ctx* ctx, int fmt, int S2, const MmqPlan& cls, int64_t
     hipFunction_t f = mmq_kernel(ctx, fmt, L, f32_in, dots);
     int64_t best_rounds = -1;
     MmqPlan best = L;
-    for (int tr = 1; tr * L.ks <= 16; tr *= 2) {
+    for (int tr = 1; tr * L.ks <= max_waves; tr *= 2) {
         MmqPlan c = L;
         c.tr = tr;
         mmq_layout(fmt, S2, dots, c);
@@ -869,12 +887,25 @@ rq_status mmq_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, const fl
     const int S2 = ws[0]->S2;
     int64_t tiles = 0;
     for (int i = 0; i < count; i++) tiles += ws[i]->tiles;
+    // A Q6_K head sums in another order than the weights beside it would take
+    // it: such a launch runs as one launch per weight, so that every output
+    // stays bit-identical to its weight's own launch.
+    int heads = 0;
+    for (int i = 0; i < count; i++) heads += q6_head(ws[i], m) ? 1 : 0;
+    if (heads > 0 && heads < count) {
+        for (int i = 0; i < count; i++) {
+            rq_status st = mmq_launch(ctx, xq, xd, xf, m, ws + i, outs + i, 1, dots);
+            if (st != RQ_OK) return st;
+        }
+        return RQ_OK;
+    }
+    const bool head = heads == count;
     // The plan of a launch of nc columns: the 16-column classes where they
     // apply and their staging fits, else the 8-column ones (up to 32).
     auto plan_for = [&](int nc) {
-        MmqPlan L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots);
+        MmqPlan L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc), tiles, xf != nullptr, dots, head);
         if (L.mp == 16 && L.lds > ctx->lds_wide)
-            L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc, false), tiles, xf != nullptr, dots);
+            L = mmq_plan(ctx, fmt, S2, mmq_cols(fmt, S2, nc, false), tiles, xf != nullptr, dots, head);
         return L;
     };
     const int max_cols = (xf || dots) ? (xf ? 1 : 8) : mmq_max_cols(fmt, S2);
@@ -1264,6 +1295,8 @@ extern "C" rq_status rq_open(int device, rq_ctx** out) {
             }
         }
     }
+    if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmq[RQ_FMT_Q6_K][0][2], "rq_mmq_q6_k_1_8");
+    if (st == RQ_OK) st = getm(ctx->mmq_mod, &ctx->mmqf[RQ_FMT_Q6_K][2], "rq_mmqf_q6_k_8");
     for (int f = 0; f < RQ_NUM_FMTS && st == RQ_OK; f++) {
         for (int gi = 0; gi < (f == RQ_FMT_Q6_K ? 1 : 3) && st == RQ_OK; gi++) {  // Q6_K: 16 x 1, sbw 4 only
             for (int si = f == RQ_FMT_Q6_K ? 1 : 0; si < 2 && st == RQ_OK; si++) {

@@ -1482,6 +1482,14 @@ RQ_MMQ_SET(q4_k, RQ_FMT_Q4_K, 8)
 // Q6_K holds 48 B of codes per lane per super-block: sbw = 8 would need 96 registers of them.
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 2)
 RQ_MMQ_SET(q6_k, RQ_FMT_Q6_K, 4)
+// One column of Q6_K at 8 super-blocks per wave: 512-thread workgroups, whose
+// two waves per SIMD may hold the 24 code loads per lane in registers.
+extern "C" __global__ __launch_bounds__(512) void rq_mmq_q6_k_1_8(RqMmqParams p) {
+    mmq_run<RQ_FMT_Q6_K, 1, 8, false, false>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void rq_mmqf_q6_k_8(RqMmqParams p) {
+    mmq_run<RQ_FMT_Q6_K, 1, 8, true, false>(p);
+}
 RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 6, 4)
 RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 8, 4)
 // Fused gate/up + activation + Q8_1 of the product (the reference's

@@ -150,6 +150,44 @@ def test_mmq_many_targets(mfma, orc, t, m):
         orc.assert_close(f"target {n}", orc.matvec_q8_1(t, w, n, k, qs, d, m), mfma.to_host(o, m * n), TOL_B)
 
 
+@pytest.mark.parametrize("k", [2560, 4096])
+def test_mmq_q6_k_head(mfma, orc, k):
+    """A Q6_K vocabulary head at one column (16384 rows of 10 and 16
+    super-blocks: 8 super-blocks per wave in 512-thread workgroups): within
+    1e-3 of the oracle; f32 columns quantized while staging bit-identical to
+    their Q8_1; beside a smaller Q6_K or a Q4_K weight in one matvec_many /
+    matmul_many call (run as a launch per weight), every output bit-identical
+    to its weight's own launch."""
+    n = 16384
+    hw = make_weight(orc, 14, n, k, 900 + k, "random")
+    head = upload(mfma, 14, hw, n, k)
+    x = orc.normal(901 + k, k, 0.0, 1.0)
+    xd = mfma.from_host(x)
+    xq = mfma.quantize_q8_1(xd, 1, k)
+    qs, d, _ = orc.quantize_q8_1(x, 1, k)
+    assert np.array_equal(xq.qs.cpu().numpy(), qs)
+    alone, f32 = mfma.alloc(n), mfma.alloc(n)
+    mfma.matvec(xq, head, alone, 1)
+    orc.assert_close(f"Q6_K head {n}x{k}", orc.matvec_q8_1(14, hw, n, k, qs, d, 1), mfma.to_host(alone, n), TOL_B)
+    mfma.matmul(xd, head, f32, 1)
+    bits = mfma.to_host(alone, n).view(np.uint32)
+    assert np.array_equal(mfma.to_host(f32, n).view(np.uint32), bits)
+    for t in (14, 12):
+        ow = make_weight(orc, t, 1024, k, 902 + t, "random")
+        other = upload(mfma, t, ow, 1024, k)
+        own = mfma.alloc(1024)
+        mfma.matvec(xq, other, own, 1)
+        own_bits = mfma.to_host(own, 1024).view(np.uint32)
+        for many in ("matvec_many", "matmul_many"):
+            outs = [mfma.alloc(1024), mfma.alloc(n)]
+            if many == "matvec_many":
+                mfma.matvec_many(xq, [other, head], outs, 1)
+            else:
+                mfma.matmul_many(xd, [other, head], outs, 1)
+            assert np.array_equal(mfma.to_host(outs[0], 1024).view(np.uint32), own_bits), (many, t)
+            assert np.array_equal(mfma.to_host(outs[1], n).view(np.uint32), bits), (many, t)
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_matmul_many_mixed_families(gpu, orc, m):
     """Backend::matmul_many over weights of both layouts: runs split where the family changes."""
