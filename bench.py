@@ -742,6 +742,7 @@ MARKS_MV = ["start", "loads issued", "staged", "arithmetic done", "stored", "pre
 MARKS_MMQT = ["start", "first loads issued", "group 0 staged", "group 0 products", "group 0 stored", "group 1 staged",
               "group 1 products", "group 1 stored"]
 MARKS_GLU = ["start", "loads issued", "staged", "last tile's arithmetic", "g and u in LDS", "stored"]
+MARKS_MMQ = ["start", "loads issued", "staged", "products done", "partials stored", "reduced and stored"]
 # The decode step's q/k/v launch (one matvec_many, LAYER's first three weights).
 QKV_SHAPES = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096)]
 
@@ -834,8 +835,12 @@ def timeline(argv) -> int:
                 which = obj
                 break
         if which is None:
-            raise RuntimeError("no instrumented kernel ran (the timeline covers rq_mvx*, rq_glu*, rq_mmq_*_16x*)")
-        names = MARKS_GLU if kind == "glu" else (MARKS_MV if which == 0 else MARKS_MMQT)
+            raise RuntimeError("no instrumented kernel ran (the timeline covers rq_mvx*, rq_glu*, and the MFMA "
+                               "classes but Q6_K's 16-column ones)")
+        if which == 0:
+            names = MARKS_GLU if kind == "glu" else MARKS_MV
+        else:  # the 16-column classes (Q4_0, Q8_0, Q4_K over 9 to 64 columns) or the others
+            names = MARKS_MMQT if kind == "matvec" and M > 8 and shapes[0][0] != 14 else MARKS_MMQ
         # Stamps of 0 are marks the kernel did not reach (an MFMA launch of
         # one column group has no group-1 marks).
         sel = live[:, :len(names)]

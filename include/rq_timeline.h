@@ -3,8 +3,8 @@
  * --timeline loads in a child process. No counterpart in the reference: a
  * measurement aid, not part of the drop-in ABI of include/rq.h.
  *
- * Each instrumented kernel (the dot4 matvecs rq_mvx_*, the int8-MFMA
- * 16-column classes rq_mmq_*_16x*) keeps up to
+ * Each instrumented kernel (the dot4 matvecs rq_mvx_* and GLU rq_glu_*, the
+ * int8-MFMA classes rq_mmq*_* but Q6_K's 16-column ones) keeps up to
  * RQ_TL_MARKS stamps of the GPU's 100 MHz real-time counter per wave and
  * stores them at its end into its code object's array of RQ_TL_SLOTS slots
  * (slot = workgroup * waves per workgroup + wave, RQ_TL_MARKS u64 each);

@@ -450,6 +450,11 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr int NLD = LPS * SBW;             // code loads per lane
     constexpr int NH = MP == 1 ? SBW / 2 : SBW;  // header loads per lane
     constexpr int NACC = MP == 8 ? 2 : 1;
+    // Timeline marks (librq_tl.so only): 0 start, 1 weight loads issued,
+    // 2 group 0 staged, 3 group 0 products done, 4 partial sums stored,
+    // 5 reduced and stored.
+    RqTl tlm;
+    tl_mark(tlm, 0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -513,6 +518,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     };
     load_w();
     __builtin_amdgcn_sched_barrier(0);
+    tl_mark(tlm, 1);
 
     // Q4_K: the lane's decoded headers (q4k_decode), filled by column group 0
     // at each super-block's first D-group and reused by the later groups.
@@ -523,6 +529,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
     mmq_stage<FMT, MP, F32IN, DOTS>(P, gi, x0, q0);
+    if (gi == 0) tl_mark(tlm, 2);
     float y[NACC];
 #pragma unroll
     for (int e = 0; e < NACC; e++) y[e] = 0.f;
@@ -707,13 +714,20 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
         }
     }
     }  // passes
+    if (gi == 0) tl_mark(tlm, 3);
     if (!DOTS) mmq_part_store<MP, NACC>(P, y, wave * G + gi, lane);
     }  // column groups
-    if (DOTS) return;
+    tl_mark(tlm, 4);
+    if (DOTS) {
+        tl_store(tlm);
+        return;
+    }
     if (GLU)
         mmq_reduce_glu<MP, G, NACC>(P, T);
     else
         mmq_reduce<MP, G, NACC>(P, T);
+    tl_mark(tlm, 5);
+    tl_store(tlm);
 }
 
 // ---------------------------------------------------------------------------
@@ -1088,6 +1102,9 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     constexpr int NACC = MP == 8 ? 2 : 1;
     static_assert(SBW == 2 || SBW == 4 || SBW == 8, "Q6_K: the d load takes 2, 4 or 8 super-blocks");
     constexpr int NA = MP == 1 ? 4 : (MP == 4 ? 1 : 2);  // A register sets (phases)
+    // Timeline marks as mmq_body's.
+    RqTl tlm;
+    tl_mark(tlm, 0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1114,6 +1131,17 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     const int np = WIDE ? max(1, P.np) : 1;
     int sb0 = kpart * SBW;
     int nsb = min(SBW, S2 - sb0);
+    // One Q8_1 column read directly (DX): with its weights, each wave loads
+    // from global memory the A operand's codes of its super-blocks (the
+    // lane's 16 of its live phase) and its two blocks' f16 scales per
+    // super-block. The column is small and every workgroup reads it, so it
+    // comes from L2. Nothing is staged in LDS, so no workgroup barrier holds
+    // a wave's products until every wave has issued its loads. The codes and
+    // scales are the staged ones, so the sums are the same bit for bit.
+    constexpr bool DX = MP == 1 && !F32IN && !DOTS && !WIDE && G == 1;
+    const int xph = g == (n & 3) ? n >> 2 : 0;  // the lane's phase (live lanes; 0 elsewhere)
+    int4 xv[DX ? SBW : 1];
+    u32 xs[DX ? SBW : 1];
 
     // ---- Round 0 of the staging loads, then the weight loads: the row's d
     // of the part's super-blocks (one load; the d rows are padded to a
@@ -1123,7 +1151,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     QF q0;
     if (F32IN) {
         qf_load(P, tid >> 2, q0);
-    } else {
+    } else if (!DX) {
         xb_load(P, tid % MP, tid / MP, x0);
     }
     u32 dw[SBW / 2];
@@ -1152,6 +1180,11 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
         for (int i = 0; i < SBW; i++) {
             const int s = min(i, nsb - 1);
+            if constexpr (DX) {  // clamped to a real super-block; zeroed past k where used
+                const int64_t sb = min(sb0 + s, (P.k >> 8) - 1);
+                xv[i] = ld16(P.xq + sb * 256 + 64 * xph + 16 * g);
+                xs[i] = *(const __attribute__((address_space(1))) u32*)(P.xd + sb * 8 + 2 * g);
+            }
             if (MP == 1)
                 h1[i] = ld4_nt(hb + s * 256);
             else
@@ -1162,10 +1195,12 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     };
     load_w();
     __builtin_amdgcn_sched_barrier(0);
+    tl_mark(tlm, 1);
 
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-    mmq_stage<FMT, MP, F32IN, DOTS>(P, gi, x0, q0);
+    if constexpr (!DX) mmq_stage<FMT, MP, F32IN, DOTS>(P, gi, x0, q0);
+    if (gi == 0) tl_mark(tlm, 2);
     float y[NACC];
 #pragma unroll
     for (int e = 0; e < NACC; e++) y[e] = 0.f;
@@ -1207,9 +1242,15 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
             for (int e = 0; e < NACC; e++) acc[e] = 0.f;
             if (MP == 1) {
+                const bool xok = !DX || sb0 + i < (P.k >> 8);  // wave-uniform
 #pragma unroll
                 for (int w = 0; w < 4; w++)
-                    if (myph == w) A[w] = lds16(xoff + 256 * i);
+                    if (myph == w) {
+                        if constexpr (DX)
+                            A[w] = xok ? v4i{xv[i].x, xv[i].y, xv[i].z, xv[i].w} : v4i{0, 0, 0, 0};
+                        else
+                            A[w] = lds16(xoff + 256 * i);
+                    }
                 v4i D = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
 #pragma unroll
                 for (int w = 0; w < 4; w++) {
@@ -1228,7 +1269,11 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
                     }
                     continue;
                 }
-                const float2 p = *(const float2*)(plb + 4 * 8 * i);
+                float2 p;
+                if constexpr (DX)
+                    p = xok ? make_float2(half_f(xs[i], 0), half_f(xs[i], 1)) : make_float2(0.f, 0.f);
+                else
+                    p = *(const float2*)(plb + 4 * 8 * i);
                 acc[0] = fmaf(p.x, (float)q6_pair(h1[i], 0, 1, D[0], D[1]),
                               p.y * (float)q6_pair(h1[i], 2, 3, D[2], D[3]));
             } else {
@@ -1283,6 +1328,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
         }
     }
     }  // passes
+    if (gi == 0) tl_mark(tlm, 3);
     if (!DOTS) {
 #pragma unroll
         for (int e = 0; e < NACC; e++) y[e] *= 0.25f;
@@ -1294,11 +1340,17 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
         }
     }
     }  // column groups
-    if (DOTS || GroupReduce<G>::on) return;
+    tl_mark(tlm, 4);
+    if (DOTS || GroupReduce<G>::on) {
+        tl_store(tlm);
+        return;
+    }
     if (GLU)
         mmq_reduce_glu<MP, G, NACC>(P, T);
     else
         mmq_reduce<MP, G, NACC>(P, T);
+    tl_mark(tlm, 5);
+    tl_store(tlm);
 }
 
 // 16-column groups over Q6_K (rq_mmq_q6_k_16x<g>_4): mmqt_body's scheme with
