@@ -747,6 +747,25 @@ MARKS_MMQ = ["start", "loads issued", "staged", "products done", "partials store
 QKV_SHAPES = [(12, 4096, 4096), (12, 1024, 4096), (14, 1024, 4096)]
 
 
+def decode_only(argv) -> int:
+    """bench.py --decode-only FAMILY [M]: the 8B-shape decode step of M
+    tokens (default 1) on FAMILY ("dot4" or "mfma") weights, Q8_1 inputs from
+    the producers (bench_decode), nothing else, so that a kernel trace of it
+    holds only the step's launches. One JSON line."""
+    import torch
+
+    from oracle import oracle as orc
+    from rllm_amd.backend import HipBackend
+
+    fam, m = argv[0], int(argv[1]) if len(argv) > 1 else 1
+    gpu = HipBackend(0)
+    d = bench_decode(torch, gpu, orc, 5, 1, m, fam, variants=(True,))
+    print(json.dumps({"decode_step": {"kernels": fam, "batch": m, "us": round(d["us"], 1), "tok_s": round(d["tok_s"], 1),
+                                      "spread_us": d["spread"]}}))
+    gpu.close()
+    return 0
+
+
 def matmul_routes(argv) -> int:
     """bench.py --matmul-routes TYPE ROWS COLS M: rq_matmul of M f32 columns
     through both routes (bench_matmul_routes), nothing else, so that a kernel
@@ -1020,6 +1039,8 @@ def main() -> int:
         return timeline(sys.argv[sys.argv.index("--timeline") + 1:])
     if "--matmul-routes" in sys.argv:
         return matmul_routes(sys.argv[sys.argv.index("--matmul-routes") + 1:])
+    if "--decode-only" in sys.argv:
+        return decode_only(sys.argv[sys.argv.index("--decode-only") + 1:])
     if "--floor-shapes" in sys.argv:
         return floor_shapes(sys.argv[sys.argv.index("--floor-shapes") + 1:])
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
