@@ -1158,7 +1158,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     int4 wv[NLD];
     int4 hv[MP == 1 ? 1 : SBW];
     u32 h1[MP == 1 ? SBW : 1];
-    auto load_w = [&]() {
+    auto load_d = [&]() {
         const int DS = (S2 + 7) & ~7;
         const u8* dp = T.hdr + (int64_t)T.tiles * S2 * 256 + ((int64_t)(tile_c * 16 + n) * DS + sb0) * 2;
         if constexpr (SBW == 2) {
@@ -1174,11 +1174,13 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
             dw[2] = (u32)v.z;
             dw[3] = (u32)v.w;
         }
+    };
+    // Super-block i's loads: (DX) its column slice, its scales, its codes.
+    auto load_sb = [&](int i) {
         const int nvalid = nsb * 3;
         const u8* cb = T.code + ((int64_t)tile_c * 3 * S2 + (int64_t)sb0 * 3) * 1024 + lane * 16;
         const u8* hb = T.hdr + ((int64_t)tile_c * S2 + sb0) * 256 + n * 16 + (MP == 1 ? 4 * g : 0);
-#pragma unroll
-        for (int i = 0; i < SBW; i++) {
+        {
             const int s = min(i, nsb - 1);
             if constexpr (DX) {  // clamped to a real super-block; zeroed past k where used
                 const int64_t sb = min(sb0 + s, (P.k >> 8) - 1);
@@ -1193,7 +1195,34 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
             for (int j = 0; j < 3; j++) wv[3 * i + j] = ld16_nt(cb + (int64_t)min(3 * i + j, nvalid - 1) * 1024);
         }
     };
-    load_w();
+    auto load_w = [&]() {
+        load_d();
+#pragma unroll
+        for (int i = 0; i < SBW; i++) load_sb(i);
+    };
+    // Staged columns (PIPE): the row's d and the first super-block's loads
+    // go out before the staging, each later super-block's while column group
+    // 0 computes the one before it. Issued all at once, the weight loads held
+    // each wave's issue back for up to ~8 us at 4096 x 14336, and the staging
+    // (its later rounds of loads wait for every load issued before them, and
+    // its barrier for every wave) started only after the whole stream, with
+    // no arithmetic overlapping it (4096 x 14336 at 4 / 8 / 16 / 32 columns:
+    // 12.8 / 15.8 / 24.0 / 39.6 -> 11.4 / 13.7 / 21.7 / 37.6 us). Not where
+    // the staging is short, 4 KB of a 4096-wide column at mp <= 4 (the
+    // 128256 x 4096 head at 4 columns 62.0 -> 63.3 us; at 8, 72.8 -> 69.3),
+    // nor in the 8 x 6 / 8 x 8 classes, whose weights spill (48 / 64 columns
+    // 55.7 / 72.3 -> 57.3 / 74.0 us), nor for one f32 column (the decode
+    // step on f32 inputs 1184 -> 1203 us). The direct column (DX) has no
+    // staging and the wide kernels walk the row in passes: they load
+    // everything at once.
+    constexpr bool PIPE = MP > 1 && !DX && !WIDE && G <= 4;
+    const bool pipe = PIPE && (MP == 8 || S2 > 16);  // wave-uniform
+    if (pipe) {
+        load_d();
+        load_sb(0);
+    } else {
+        load_w();
+    }
     __builtin_amdgcn_sched_barrier(0);
     tl_mark(tlm, 1);
 
@@ -1237,6 +1266,10 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
         for (int i = 0; i < SBW; i++) {
             if (i >= nsb) break;  // a short last k-part (uniform)
+            if (pipe && gi == 0 && i + 1 < SBW) {
+                load_sb(i + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             const float dsb = half_f(dw[i >> 1], i & 1);
             float acc[NACC];
 #pragma unroll
