@@ -503,20 +503,36 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     constexpr int LPH = NLD / NH;  // code loads per header
     int4 wv[NLD];
     int4 hv[NH];
-    auto load_w = [&]() {
+    // Header i and its code loads.
+    auto load_h = [&](int i) {
         const int nvalid = nsb * LPS;
         const u8* cb = T.code + ((int64_t)tile_c * LPS * S2 + (int64_t)sb0 * LPS) * 1024 + lane * 16;
         const u8* hb = T.hdr + ((int64_t)tile_c * S2 + sb0) * 256 + n * 16;
+        const int s = MP == 1 ? 2 * i + (g >> 1) : i;
+        hv[i] = ld16_nt(hb + min(s, nsb - 1) * 256);
 #pragma unroll
-        for (int i = 0; i < NH; i++) {
-            const int s = MP == 1 ? 2 * i + (g >> 1) : i;
-            hv[i] = ld16_nt(hb + min(s, nsb - 1) * 256);
-#pragma unroll
-            for (int j = 0; j < LPH; j++)
-                wv[i * LPH + j] = ld16_nt(cb + (int64_t)min(i * LPH + j, nvalid - 1) * 1024);
-        }
+        for (int j = 0; j < LPH; j++)
+            wv[i * LPH + j] = ld16_nt(cb + (int64_t)min(i * LPH + j, nvalid - 1) * 1024);
     };
-    load_w();
+    auto load_w = [&]() {
+#pragma unroll
+        for (int i = 0; i < NH; i++) load_h(i);
+    };
+    // The 8-column classes (PIPE): the first super-block's loads go out
+    // before the staging, each later one's while column group 0 computes the
+    // one before it, as in mmq6_body, where the staging's later rounds of
+    // loads and its barrier otherwise waited for the whole weight stream
+    // (Q4_K 14336 x 4096 at 8 columns 10.0 -> 8.9 us, Q8_0 11008 x 4096
+    // 12.6 -> 11.6, the fused FFN front 21.3 -> 19.2-19.9). Not at 4 columns,
+    // whose 4 KB columns of k = 4096 stage quickly, and where a run-time
+    // choice cost the launches that did not take it (Q4_K 14336 x 4096 at 2 /
+    // 4 columns 8.3 / 8.7 -> 8.8 / 9.1 us).
+    constexpr bool PIPE = MP == 8 && !WIDE && G <= 4;
+    const bool pipe = PIPE;
+    if (pipe)
+        load_h(0);
+    else
+        load_w();
     __builtin_amdgcn_sched_barrier(0);
     tl_mark(tlm, 1);
 
@@ -566,6 +582,10 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
         for (int t = 0; t < ND; t++) {
             if (t * NPH * 64 >= nsb * 256) break;  // a short last k-part (uniform)
+            if (pipe && gi == 0 && (t * NPH) % 4 == 0 && (t * NPH) / 4 + 1 < NH) {
+                load_h((t * NPH) / 4 + 1);  // the next super-block (mp >= 2: header i = super-block i)
+                __builtin_amdgcn_sched_barrier(0);
+            }
             // Two accumulator chains (phases of either half) halve the
             // dependent MFMA latency; their slots do not overlap, so the sum
             // is exact.
