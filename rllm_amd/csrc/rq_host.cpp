@@ -713,10 +713,12 @@ hipFunction_t mmq_kernel(const rq_ctx* ctx, int fmt, const MmqPlan& L, bool f32_
     return f32_in ? ctx->mmqf[fi][si] : ctx->mmq[fi][mi][si];
 }
 
-// End of a 16-column layout's activation planes (block-major f16 scales;
+// End of a 16-column layout's activation planes (block-major scales: f32 in
+// the Q4_K / Q4_0 matvec classes, f16 in the others and the fused FFN's;
 // Q4_K / Q4_0 also f = dx sum q in f32).
-int mmqt_planes_end(int fmt, int S2, const MmqPlan& L) {
-    return L.pl_off + 8 * S2 * 16 * (fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q4_0 ? 6 : 2);
+int mmqt_planes_end(int fmt, int S2, const MmqPlan& L, bool glu) {
+    const bool q4 = fmt == RQ_FMT_Q4_K || fmt == RQ_FMT_Q4_0;
+    return L.pl_off + 8 * S2 * 16 * ((q4 && !glu ? 4 : 2) + (q4 ? 4 : 0));
 }
 
 void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
@@ -732,7 +734,7 @@ void mmq_layout(int fmt, int S2, bool dots, MmqPlan& L) {
         // workgroups to a CU, and the planner's fewer tiles per workgroup ran
         // slower: Q4_K 14336 x 4096 at 16 / 32 / 64 columns 11.7 / 19.3 /
         // 34.4 -> 13.3 / 22.4 / 41.1 us.)
-        L.part_off = mmqt_planes_end(fmt, S2, L);
+        L.part_off = mmqt_planes_end(fmt, S2, L, false);
         L.lds = L.part_off + L.ks * L.tr * 64 * 4 * 4;
         return;
     }
@@ -1013,7 +1015,7 @@ rq_status mmq_glu_launch(rq_ctx* ctx, const int8_t* xq, const uint16_t* xd, cons
         // 16-column workgroups: both weights' partial sums of one group
         // (over the staged codes where they fit there), then h of one group.
         auto glu16 = [&]() {
-            const int planes_end = mmqt_planes_end(fmt, S2, L), pb = 2 * L.ks * L.tr * 64 * 4 * 4;
+            const int planes_end = mmqt_planes_end(fmt, S2, L, true), pb = 2 * L.ks * L.tr * 64 * 4 * 4;
             L.part_off = pb <= L.pl_off ? 0 : planes_end;
             h_off = L.part_off == 0 ? planes_end : planes_end + pb;
             L.lds = h_off + 16 * 32 * 4;

@@ -106,18 +106,23 @@ __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b,
     if (DOTS) *(int*)(pl + NPL * stride) = sq;
 }
 
-// The 16-column classes (mmqt_body) keep their planes block-major: the f16
-// activation scale dx of block b, column a at pl_off + ((b / 2) * 16 + a) *
-// 4 + (b % 2) * 2 (a lane reads four columns' scales of both blocks of a
-// window in 16 bytes), and, for Q4_K and Q4_0, f = dx sum q as f32 at
-// pl_off + 8 * S2 * 16 * 2 + (b * 16 + a) * 4 (consecutive columns: the
+// The 16-column classes (mmqt_body) keep their planes block-major: the
+// activation scale dx of block b, column a, as f16 at pl_off + ((b / 2) * 16
+// + a) * 4 + (b % 2) * 2 (a lane reads four columns' scales of both blocks of
+// a window in 16 bytes) or, F32DX, as f32 at pl_off + (b * 16 + a) * 4 (a
+// lane reads four columns' scales of one block in 16 bytes, and converts
+// none per entry), and, for Q4_K and Q4_0, f = dx sum q as f32 at pl_off +
+// 8 * S2 * 16 * (2 or 4) + (b * 16 + a) * 4 (consecutive columns: the
 // correction MFMA's A operand).
-template <int FMT>
+template <int FMT, bool F32DX = false>
 __device__ __forceinline__ void stage_planes_t(const RqMmqParams& P, int a, int b, int sq, u32 d16) {
     char* pl = mmq_lds + P.pl_off;
-    *(u16*)(pl + ((b >> 1) * 16 + a) * 4 + (b & 1) * 2) = (u16)d16;
-    if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0)
-        ((float*)(pl + 8 * P.S2 * 16 * 2))[b * 16 + a] = h2f(d16) * (float)sq;  // exact: f16 times |sq| <= 4064
+    if (F32DX)
+        ((float*)pl)[b * 16 + a] = h2f(d16);
+    else
+        *(u16*)(pl + ((b >> 1) * 16 + a) * 4 + (b & 1) * 2) = (u16)d16;
+    if (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0)  // exact: f16 times |sq| <= 4064
+        ((float*)(pl + 8 * P.S2 * 16 * (F32DX ? 4 : 2)))[b * 16 + a] = h2f(d16) * (float)sq;
 }
 
 // One Q8_1 block (codes and f16 scale) in registers. The loads are
@@ -140,7 +145,7 @@ __device__ __forceinline__ void xb_load(const RqMmqParams& P, int a, int b, XB& 
     x.d16 = P.xd[(int64_t)ac * U + bc];
 }
 
-template <int FMT, int MP, bool DOTS, bool TP = false>
+template <int FMT, int MP, bool DOTS, bool TP = false, bool F32DX = false>
 __device__ __forceinline__ void xb_write(const RqMmqParams& P, int a, int b, XB x) {
     if (!x.valid) {
         x.lo = make_int4(0, 0, 0, 0);
@@ -160,7 +165,7 @@ __device__ __forceinline__ void xb_write(const RqMmqParams& P, int a, int b, XB 
     *(int4*)xp = x.lo;
     *(int4*)(xp + 16) = x.hi;
     if constexpr (TP)
-        stage_planes_t<FMT>(P, a, b, sq, x.d16);
+        stage_planes_t<FMT, F32DX>(P, a, b, sq, x.d16);
     else
         stage_planes<FMT, MP, DOTS>(P, a, b, sq, h2f(x.d16));
 }
@@ -814,19 +819,19 @@ __device__ __forceinline__ void mmqt_prefetch(const RqMmqParams& P, int gi, XB& 
 }
 
 // Staging of column group gi between barriers, from its prefetched rounds.
-template <int FMT>
+template <int FMT, bool F32DX>
 __device__ __forceinline__ void mmqt_stage(const RqMmqParams& P, int gi, const XB& x0, const XB& x1) {
     const int threads = blockDim.x, tid = threadIdx.x, items = 16 * 8 * P.S2;
     if (gi > 0) __syncthreads();  // the previous group's LDS reads are done
     int it = tid;
-    if (it < items) xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x0);
+    if (it < items) xb_write<FMT, 16, false, true, F32DX>(P, it & 15, it >> 4, x0);
     it += threads;
-    if (it < items) xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x1);
+    if (it < items) xb_write<FMT, 16, false, true, F32DX>(P, it & 15, it >> 4, x1);
     it += threads;
     for (; it < items; it += threads) {
         XB x;
         xb_load(P, gi * 16 + (it & 15), it >> 4, x);
-        xb_write<FMT, 16, false, true>(P, it & 15, it >> 4, x);
+        xb_write<FMT, 16, false, true, F32DX>(P, it & 15, it >> 4, x);
     }
     __syncthreads();
 }
@@ -959,14 +964,19 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
             mk[par][h] = AMASK || (g >> 1) == h ? m : 0u;
         }
 
-    const char* dxp = mmq_lds + P.pl_off;                          // f16 dx, [block pair][16][2]
-    const float* fpl = (const float*)(mmq_lds + P.pl_off + NB * 16 * 2);  // f32 f, [block][16]
+    // The Q4_K / Q4_0 matvec classes stage f32 scales (F32DX: one VALU less
+    // per entry). The fused FFN's keep f16, whose smaller planes fit two of
+    // its workgroups to a CU at k = 4096, and so do Q8_0's (with f32 its two-
+    // group class spilled 36 bytes).
+    constexpr bool F32DX = !GLU && (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0);
+    const char* dxp = mmq_lds + P.pl_off;  // dx: f32 [block][16], or f16 [block pair][16][2]
+    const float* fpl = (const float*)(mmq_lds + P.pl_off + NB * 16 * (F32DX ? 4 : 2));  // f32 f, [block][16]
     float* part = (float*)(mmq_lds + P.part_off);
     const int ia = lane & 15;  // A row: activation ia
 
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-    mmqt_stage<FMT>(P, gi, x0, x1);
+    mmqt_stage<FMT, F32DX>(P, gi, x0, x1);
     if (gi < 2) tl_mark(tlm, 2 + 3 * gi);
     if (gi + 1 < G) mmqt_prefetch(P, gi + 1, x0, x1);
     v4f y = {0.f, 0.f, 0.f, 0.f};
@@ -1019,7 +1029,8 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
                     A = lds16(xoff + 256 * i + 64 * w);
                 }
                 // dx of activations a4 .. a4 + 3 (dwords), blocks 2w (low halves) and 2w + 1
-                const int4 dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
+                int4 dxw;  // f16 planes: both blocks of the window
+                if constexpr (!F32DX) dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
                 v4i B;
                 if (AMASK) {
                     const u32 m = mk[NIB ? (w & 1) : 0][0];
@@ -1033,18 +1044,30 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
                         B = v4i{(int)((u32)v.x & m), (int)((u32)v.y & m), (int)((u32)v.z & m), (int)((u32)v.w & m)};
                     }
                     const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(AMASK ? Ah[h] : A, B, (v4i{0, 0, 0, 0}), 0, 0, 0);
-                    const u32 dxv[4] = {(u32)dxw.x, (u32)dxw.y, (u32)dxw.z, (u32)dxw.w};
+                    float dxe[4];  // the activations' dx of block h of the window
+                    if constexpr (F32DX) {
+                        const float4 q = *(const float4*)(dxp + ((b0 + 2 * w + h) * 16 + 4 * g) * 4);
+                        dxe[0] = q.x;
+                        dxe[1] = q.y;
+                        dxe[2] = q.z;
+                        dxe[3] = q.w;
+                    } else {
+                        dxe[0] = hsel((u32)dxw.x, h);
+                        dxe[1] = hsel((u32)dxw.y, h);
+                        dxe[2] = hsel((u32)dxw.z, h);
+                        dxe[3] = hsel((u32)dxw.w, h);
+                    }
                     const int b = 2 * w + h;  // block within the super-block
                     v4f& ac = acc[NIB ? (w & 1) : 0];
                     if (FMT == RQ_FMT_Q4_K) {
                         const int sc = (int)vbyte(ksc[i][w >> 1], b & 3);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)__mul24(sc, D[e]), hsel(dxv[e], h), ac[e]);
+                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)__mul24(sc, D[e]), dxe[e], ac[e]);
                     } else {
                         const u32 wd = (u32)(w == 0 ? hv[i].x : w == 1 ? hv[i].y : w == 2 ? hv[i].z : hv[i].w);
                         const float db = half_f(wd, h);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)D[e] * hsel(dxv[e], h), db, ac[e]);
+                        for (int e = 0; e < 4; e++) ac[e] = fmaf((float)D[e] * dxe[e], db, ac[e]);
                     }
                 }
             }
@@ -1473,13 +1496,14 @@ __device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
     load_sb(0);
     __builtin_amdgcn_sched_barrier(0);
 
-    const char* dxp = mmq_lds + P.pl_off;  // f16 dx, [block pair][16][2]
+    constexpr bool F32DX = false;  // f16 planes (f32 ones spilled 36 bytes here)
+    const char* dxp = mmq_lds + P.pl_off;  // dx: f32 [block][16], or f16 [block pair][16][2]
     float* part = (float*)(mmq_lds + P.part_off);
     const int ia = lane & 15;
 
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-    mmqt_stage<FMT>(P, gi, x0, x1);
+    mmqt_stage<FMT, F32DX>(P, gi, x0, x1);
     if (gi + 1 < G) mmqt_prefetch(P, gi + 1, x0, x1);
     v4f y = {0.f, 0.f, 0.f, 0.f};
 
@@ -1503,16 +1527,29 @@ __device__ __forceinline__ void mmqt6_body(const RqMmqParams& P) {
 #pragma unroll
                 for (int c = 0; c < 4; c++)
                     if (g == c) A[c] = lds16(xoff + 256 * i + 64 * w);
-                const int4 dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
-                const u32 dxv[4] = {(u32)dxw.x, (u32)dxw.y, (u32)dxw.z, (u32)dxw.w};
+                int4 dxw;  // f16 planes: both blocks of the window
+                if constexpr (!F32DX) dxw = *(const int4*)(dxp + (((b0 >> 1) + w) * 16 + 4 * g) * 4);
                 const u32 sc = (u32)(w == 0 ? hv[i].x : w == 1 ? hv[i].y : w == 2 ? hv[i].z : hv[i].w);
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     const v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2 * h], B, (v4i{0, 0, 0, 0}), 0, 0, 0);
                     const v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2 * h + 1], B, (v4i{0, 0, 0, 0}), 0, 0, 0);
+                    float dxe[4];  // the activations' dx of block h of the window
+                    if constexpr (F32DX) {
+                        const float4 q = *(const float4*)(dxp + ((b0 + 2 * w + h) * 16 + 4 * g) * 4);
+                        dxe[0] = q.x;
+                        dxe[1] = q.y;
+                        dxe[2] = q.z;
+                        dxe[3] = q.w;
+                    } else {
+                        dxe[0] = hsel((u32)dxw.x, h);
+                        dxe[1] = hsel((u32)dxw.y, h);
+                        dxe[2] = hsel((u32)dxw.z, h);
+                        dxe[3] = hsel((u32)dxw.w, h);
+                    }
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        acc[e] = fmaf((float)q6_pair(sc, 2 * h, 2 * h + 1, Da[e], Db[e]), hsel(dxv[e], h), acc[e]);
+                        acc[e] = fmaf((float)q6_pair(sc, 2 * h, 2 * h + 1, Da[e], Db[e]), dxe[e], acc[e]);
                 }
             }
             y += (0.25f * half_f(dw[i >> 1], i & 1)) * acc;
