@@ -110,8 +110,8 @@ __device__ __forceinline__ void stage_planes(const RqMmqParams& P, int a, int b,
 // activation scale dx of block b, column a, as f16 at pl_off + ((b / 2) * 16
 // + a) * 4 + (b % 2) * 2 (a lane reads four columns' scales of both blocks of
 // a window in 16 bytes) or, F32DX, as f32 at pl_off + (b * 16 + a) * 4 (a
-// lane reads four columns' scales of one block in 16 bytes, and converts
-// none per entry), and, for Q4_K and Q4_0, f = dx sum q as f32 at pl_off +
+// lane reads four columns' scales of one block in 16 bytes), and, for Q4_K
+// and Q4_0, f = dx sum q as f32 at pl_off +
 // 8 * S2 * 16 * (2 or 4) + (b * 16 + a) * 4 (consecutive columns: the
 // correction MFMA's A operand).
 template <int FMT, bool F32DX = false>
@@ -964,10 +964,13 @@ __device__ __forceinline__ void mmqt_body(const RqMmqParams& P) {
             mk[par][h] = AMASK || (g >> 1) == h ? m : 0u;
         }
 
-    // The Q4_K / Q4_0 matvec classes stage f32 scales (F32DX: one VALU less
-    // per entry). The fused FFN's keep f16, whose smaller planes fit two of
-    // its workgroups to a CU at k = 4096, and so do Q8_0's (with f32 its two-
-    // group class spilled 36 bytes).
+    // The Q4_K / Q4_0 matvec classes stage f32 scales (F32DX), read per MFMA
+    // as the four entries' 16 bytes: fewer live registers than a window's
+    // f16 pairs, so the four-group class no longer spills (the f16 form
+    // converts inside v_fma_mix_f32, so neither costs a VALU per entry). The
+    // fused FFN's keep f16, whose smaller planes fit two of its workgroups to
+    // a CU at k = 4096, and so do Q8_0's (with f32 its two-group class
+    // spilled 36 bytes).
     constexpr bool F32DX = !GLU && (FMT == RQ_FMT_Q4_K || FMT == RQ_FMT_Q4_0);
     const char* dxp = mmq_lds + P.pl_off;  // dx: f32 [block][16], or f16 [block pair][16][2]
     const float* fpl = (const float*)(mmq_lds + P.pl_off + NB * 16 * (F32DX ? 4 : 2));  // f32 f, [block][16]
