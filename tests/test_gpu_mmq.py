@@ -63,13 +63,15 @@ def test_mmq_q6_k_wide_rows_many_columns(mfma, orc, m):
 
 
 @pytest.mark.parametrize("tname", list(MMQ_TYPES))
-@pytest.mark.parametrize("k", [256, 768, 2048, 4096, 14336, 20480, 36864])
-@pytest.mark.parametrize("m", [1, 3, 8, 16, 20])
+@pytest.mark.parametrize("k", [256, 768, 2048, 2560, 4096, 13824, 14336, 20480, 36864])
+@pytest.mark.parametrize("m", [1, 3, 8, 16, 20, 32])
 def test_mmq_widths(mfma, orc, tname, k, m):
     """Odd super-block counts (zero padding to an even count), 2/4 super-blocks
-    per wave; rows of more than 64 super-blocks (past 16384 columns) in the
-    wide kernels' passes (2 and 3 passes here); 16 columns in one
-    16-column launch where the staging fits, else in 8-column groups."""
+    per wave and short last k-parts (k = 2560, 13824: a part of 2 super-blocks,
+    where the classes that load one super-block ahead clamp the next one);
+    rows of more than 64 super-blocks (past 16384 columns) in the wide
+    kernels' passes (2 and 3 passes here); 16 columns in one 16-column launch
+    where the staging fits, else in 8-column groups."""
     _run(mfma, orc, MMQ_TYPES[tname], 33, k, m, 17 * k + m, kind="normal")
 
 
