@@ -523,16 +523,15 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
         for (int i = 0; i < NH; i++) load_h(i);
     };
-    // The 8-column classes (PIPE): the first super-block's loads go out
-    // before the staging, each later one's while column group 0 computes the
-    // one before it, as in mmq6_body, where the staging's later rounds of
+    // The 4- and 8-column classes (PIPE): the first super-block's loads go
+    // out before the staging, each later one's while column group 0 computes
+    // the one before it, as in mmq6_body, where the staging's later rounds of
     // loads and its barrier otherwise waited for the whole weight stream
-    // (Q4_K 14336 x 4096 at 8 columns 10.0 -> 8.9 us, Q8_0 11008 x 4096
-    // 12.6 -> 11.6, the fused FFN front 21.3 -> 19.2-19.9). Not at 4 columns,
-    // whose 4 KB columns of k = 4096 stage quickly, and where a run-time
-    // choice cost the launches that did not take it (Q4_K 14336 x 4096 at 2 /
-    // 4 columns 8.3 / 8.7 -> 8.8 / 9.1 us).
-    constexpr bool PIPE = MP == 8 && !WIDE && G <= 4;
+    // (Q4_K 14336 x 4096 at 2 / 4 / 8 columns 8.20 / 8.80 / 10.0 -> 7.95 /
+    // 8.46 / 8.9 us, the fused FFN front at 4 / 8 columns 19.0 / 21.3 ->
+    // 15.8 / 18.6). Chosen at compile time: a run-time choice slowed the
+    // launches that did not take it.
+    constexpr bool PIPE = MP >= 4 && !WIDE && G <= 4;
     const bool pipe = PIPE;
     if (pipe)
         load_h(0);
