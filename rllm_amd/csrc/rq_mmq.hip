@@ -523,15 +523,16 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
         for (int i = 0; i < NH; i++) load_h(i);
     };
-    // The 4- and 8-column classes (PIPE): the first super-block's loads go
-    // out before the staging, each later one's while column group 0 computes
-    // the one before it, as in mmq6_body, where the staging's later rounds of
-    // loads and its barrier otherwise waited for the whole weight stream
-    // (Q4_K 14336 x 4096 at 2 / 4 / 8 columns 8.20 / 8.80 / 10.0 -> 7.95 /
-    // 8.46 / 8.9 us, the fused FFN front at 4 / 8 columns 19.0 / 21.3 ->
-    // 15.8 / 18.6). Chosen at compile time: a run-time choice slowed the
-    // launches that did not take it.
-    constexpr bool PIPE = MP >= 4 && !WIDE && G <= 4;
+    // The staged classes (PIPE): the first super-block's loads go out before
+    // the staging, each later one's while column group 0 computes the one
+    // before it, as in mmq6_body, where the staging's later rounds of loads
+    // and its barrier otherwise waited for the whole weight stream (Q4_K
+    // 14336 x 4096 at 2 / 4 / 8 columns 8.20 / 8.80 / 10.0 -> 7.95 / 8.46 /
+    // 8.9 us, the fused FFN front at 4 / 8 columns 19.0 / 21.3 -> 15.8 /
+    // 18.6; at one column the MFMA decode step 1138 -> 1111 us). Chosen at
+    // compile time: a run-time choice slowed the launches that did not take
+    // it.
+    constexpr bool PIPE = !WIDE && G <= 4;
     const bool pipe = PIPE;
     if (pipe)
         load_h(0);
@@ -586,8 +587,10 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
 #pragma unroll
         for (int t = 0; t < ND; t++) {
             if (t * NPH * 64 >= nsb * 256) break;  // a short last k-part (uniform)
-            if (pipe && gi == 0 && (t * NPH) % 4 == 0 && (t * NPH) / 4 + 1 < NH) {
-                load_h((t * NPH) / 4 + 1);  // the next super-block (mp >= 2: header i = super-block i)
+            // The next header and its codes: mp = 1 one header per D-group (two
+            // super-blocks), mp >= 2 one per super-block, (t NPH) / 4.
+            if (pipe && gi == 0 && (MP == 1 || (t * NPH) % 4 == 0) && (MP == 1 ? t : (t * NPH) / 4) + 1 < NH) {
+                load_h((MP == 1 ? t : (t * NPH) / 4) + 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // Two accumulator chains (phases of either half) halve the
@@ -1252,16 +1255,16 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     // (its later rounds of loads wait for every load issued before them, and
     // its barrier for every wave) started only after the whole stream, with
     // no arithmetic overlapping it (4096 x 14336 at 4 / 8 / 16 / 32 columns:
-    // 12.8 / 15.8 / 24.0 / 39.6 -> 11.4 / 13.7 / 21.7 / 37.6 us). Not where
-    // the staging is short, 4 KB of a 4096-wide column at mp <= 4 (the
-    // 128256 x 4096 head at 4 columns 62.0 -> 63.3 us; at 8, 72.8 -> 69.3),
-    // nor in the 8 x 6 / 8 x 8 classes, whose weights spill (48 / 64 columns
+    // 12.8 / 15.8 / 24.0 / 39.6 -> 11.4 / 13.7 / 21.7 / 37.6 us; the
+    // 128256 x 4096 head at 8 columns 72.8 -> 69.3, at 4 62.0 -> 63.3). Not
+    // in the 8 x 6 / 8 x 8 classes, whose weights spill (48 / 64 columns
     // 55.7 / 72.3 -> 57.3 / 74.0 us), nor for one f32 column (the decode
-    // step on f32 inputs 1184 -> 1203 us). The direct column (DX) has no
-    // staging and the wide kernels walk the row in passes: they load
-    // everything at once.
+    // step on f32 inputs 1184 -> 1203 us). Chosen at compile time (a run-time
+    // choice slowed the launches that did not take it). The direct column
+    // (DX) has no staging and the wide kernels walk the row in passes: they
+    // load everything at once.
     constexpr bool PIPE = MP > 1 && !DX && !WIDE && G <= 4;
-    const bool pipe = PIPE && (MP == 8 || S2 > 16);  // wave-uniform
+    const bool pipe = PIPE;
     if (pipe) {
         load_d();
         load_sb(0);
