@@ -1255,9 +1255,16 @@ def main() -> int:
         f32 = dec["f32in"]
         log(f"8B-shape decode step (f32 inputs, quantized in each call): {f32['us']:.0f} us median "
             f"({f32['spread']['min']}-{f32['spread']['max']}), {f32['tok_s']:.1f} tok/s")
+    # The same one-token step on int8-MFMA-layout weights: what serving batch 1
+    # costs when one layout (the one batched steps want) holds the model.
+    dec_mfma = None
+    if not args.no_decode:
+        dec_mfma = bench_decode(torch, gpu, orc, max(5, args.steps // 2), 2, 1, "mfma", variants=(True,))
+        log(f"8B-shape decode step on MFMA-layout weights (Q8_1 from the producers): {dec_mfma['us']:.0f} us median "
+            f"({dec_mfma['spread']['min']}-{dec_mfma['spread']['max']}), {dec_mfma['tok_s']:.1f} tok/s")
     if not args.no_decode and args.all_configs:
-        # The same step on int8-MFMA weights: one token (the cost of serving
-        # batch 1 from the MFMA layout alone) and continuous batches of m tokens.
+        # The same step on int8-MFMA weights for continuous batches of m tokens
+        # (f32 inputs as well for one token).
         for m in (1, 8, 32):
             b = bench_decode(torch, gpu, orc, 5, 1, m, "mfma")
             for how, bv in (("Q8_1 from the producers", b), ("f32 inputs", b["f32in"])):
@@ -1334,6 +1341,9 @@ def main() -> int:
         "launch_floors_us": {"empty_launch": round(empty["us"], 3),
                              "read_floor_q4k_4096x4096": round(floor_small["us"], 3)} if floor_small and empty else None,
         "decode_f32in_step_us": round(dec["f32in"]["us"], 1) if dec else None,
+        "decode_mfma_tok_s": round(dec_mfma["tok_s"], 1) if dec_mfma else None,
+        "decode_mfma_step_us": round(dec_mfma["us"], 1) if dec_mfma else None,
+        "decode_mfma_spread_us": dec_mfma["spread"] if dec_mfma else None,
         "upload_gbs": round(dec["upload_gbs"], 1) if dec else None,
         "roofline": roofline,
         "cpu_baseline": cpu,
