@@ -533,8 +533,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
     // compile time: a run-time choice slowed the launches that did not take
     // it.
     constexpr bool PIPE = !WIDE && G <= 4;
-    const bool pipe = PIPE;
-    if (pipe)
+    if constexpr (PIPE)
         load_h(0);
     else
         load_w();
@@ -589,7 +588,7 @@ __device__ __forceinline__ void mmq_body(const RqMmqParams& P) {
             if (t * NPH * 64 >= nsb * 256) break;  // a short last k-part (uniform)
             // The next header and its codes: mp = 1 one header per D-group (two
             // super-blocks), mp >= 2 one per super-block, (t NPH) / 4.
-            if (pipe && gi == 0 && (MP == 1 || (t * NPH) % 4 == 0) && (MP == 1 ? t : (t * NPH) / 4) + 1 < NH) {
+            if (PIPE && gi == 0 && (MP == 1 || (t * NPH) % 4 == 0) && (MP == 1 ? t : (t * NPH) / 4) + 1 < NH) {
                 load_h((MP == 1 ? t : (t * NPH) / 4) + 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -1264,8 +1263,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
     // (DX) has no staging and the wide kernels walk the row in passes: they
     // load everything at once.
     constexpr bool PIPE = MP > 1 && !DX && !WIDE && G <= 4;
-    const bool pipe = PIPE;
-    if (pipe) {
+    if constexpr (PIPE) {
         load_d();
         load_sb(0);
     } else {
@@ -1314,7 +1312,7 @@ __device__ __forceinline__ void mmq6_body(const RqMmqParams& P) {
 #pragma unroll
         for (int i = 0; i < SBW; i++) {
             if (i >= nsb) break;  // a short last k-part (uniform)
-            if (pipe && gi == 0 && i + 1 < SBW) {
+            if (PIPE && gi == 0 && i + 1 < SBW) {
                 load_sb(i + 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
