@@ -1639,7 +1639,9 @@ RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 6, 4)
 RQ_MMQ_G(q6_k, RQ_FMT_Q6_K, 8, 4)
 // Fused gate/up + activation + Q8_1 of the product (the reference's
 // mmq_glu_*), 4 super-blocks per wave (rows of up to 16: the two weights'
-// k-parts of two tiles fill at most 16 waves).
+// k-parts of two tiles fill at most 16 waves); one column over rows of 9 to
+// 16 super-blocks also at 8 per wave in 512-thread workgroups (_1s8 over
+// Q8_1, f_..._s8 over f32), whose waves have the registers for it.
 #define RQ_MMQ_GLU_SET(NAME, FMT)                                                                    \
     extern "C" __global__ __launch_bounds__(1024) void rq_mmqglu_##NAME##_1(RqMmqParams p) {         \
         mmq_run<FMT, 1, 4, false, false, 1, true>(p);                                                \
